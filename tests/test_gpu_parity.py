@@ -1,0 +1,155 @@
+"""Kernel-vs-oracle parity on the GPU, through the C ABI (pagedbatch_amd.sampling.sample_arrays).
+
+Every case prints its name, dtype and shape before touching the GPU, so a failure names
+itself. Bars (oracle/compare.py): greedy tokens bit-exact; stochastic tokens identical
+unless u lies within 1e-6 of a CDF boundary; kept sets identical unless top_p lies within
+1e-6 of a cumulative boundary; probabilities within 1e-5 absolute.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from oracle.compare import compare_rows
+from pagedbatch_amd import workloads
+from pagedbatch_amd.sampling import sample_arrays
+
+pytestmark = pytest.mark.gpu
+
+DT_NAME = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}
+
+
+def raw_numpy(x: torch.Tensor) -> np.ndarray:
+    if x.dtype == torch.bfloat16:
+        return x.view(torch.int16).numpy().view(np.uint16)
+    return x.numpy()
+
+
+def run_case(dev, name, logits_cpu, T, K, P, U, row_map=None, want_probs=True, info_only=False):
+    print(f"[case] {name} dtype={logits_cpu.dtype} shape={tuple(logits_cpu.shape)} rows_out={len(T)}", flush=True)
+    x = logits_cpu.to(dev)
+    out = sample_arrays(x, T, K, P, U, row_map=row_map, debug=True)
+    refs = oracle.sample_batch(raw_numpy(logits_cpu), DT_NAME[logits_cpu.dtype], T, K, P, U, row_map=row_map,
+                               want_probs=want_probs)
+    greedy = [t == 0 for t in T]
+    probs = None if info_only else out.probs.cpu().numpy()
+    kept = None if info_only else out.kept.cpu().numpy()
+    rep = compare_rows(out.tokens, out.status, refs, greedy, probs=probs, kept=kept, info=out.info)
+    print(f"[case] {name}: {rep.summary()}", flush=True)
+    assert rep.ok(), rep.summary()
+    return out, refs, rep
+
+
+def test_steps8_smollm_mixed(dev):
+    w = workloads.steps8_smollm_mixed()
+    run_case(dev, w.name, w.logits, w.temperature, w.top_k, w.top_p, w.uniform)
+
+
+def test_greedy512_quantized_bit_exact(dev):
+    w = workloads.greedy512_quantized()
+    print(f"[case] {w.name}", flush=True)
+    out = sample_arrays(w.logits.to(dev), w.temperature, w.top_k, w.top_p, w.uniform)
+    ref = np.argmax(w.logits.numpy(), axis=1)
+    assert (out[1] == 0).all()
+    np.testing.assert_array_equal(out[0], ref)
+    # the 1/4 grid puts a tie at the maximum in a good share of rows
+    x = w.logits.numpy()
+    assert ((x == x.max(axis=1, keepdims=True)).sum(axis=1) > 1).mean() > 0.25
+    # and rows with the maximum planted at several random positions, first copy not at 0
+    g = torch.Generator().manual_seed(11)
+    y = w.logits[:64].clone()
+    for r in range(64):
+        pos = torch.randperm(y.shape[1], generator=g)[: 2 + r % 7]
+        y[r, pos] = 9.0
+    out = sample_arrays(y.to(dev), [0.0] * 64, [0] * 64, [1.0] * 64, [0.0] * 64)
+    np.testing.assert_array_equal(out[0], np.argmax(y.numpy(), axis=1))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("vocab", [1, 7, 64, 1000, 4096, 32003, 65536])
+def test_random_rows(dev, dtype, vocab):
+    g = torch.Generator().manual_seed(vocab * 7 + int(DT_NAME[dtype] == "float16"))
+    rows = 24
+    x = torch.randn(rows, vocab, generator=g) * 1.5
+    x[rows // 2:] = torch.round(x[rows // 2:] * 4) / 4  # heavy ties in half the rows
+    logits = x.to(dtype)
+    T = [0.0, 0.7, 1.0, 1.3] * (rows // 4)
+    K = [0, 1, 2, 5, 50, vocab - 1, vocab, 0] * (rows // 8)
+    P = [1.0, 0.5, 0.9, 0.95, 1e-6, 0.999] * (rows // 6)
+    U = [float(v) for v in torch.rand(rows, generator=g)]
+    U[3] = 0.0
+    run_case(dev, f"random_{DT_NAME[dtype]}_{vocab}", logits, T, K, P, U)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_reference_known_answers(dev, dtype):
+    """tests/test_engine.py:86-93 of the reference, through the kernel."""
+    logits = torch.tensor([[0.1, 3.0, 0.2, 2.9]]).to(dtype)
+    x = logits.to(dev)
+    g = torch.Generator().manual_seed(0)
+    for T, K, P in [(0.0, 0, 1.0), (1.0, 1, 1.0), (1.0, 0, 1e-6)]:
+        u = float(torch.rand((), generator=g))
+        tok, st = sample_arrays(x, [T], [K], [P], [u])
+        assert st[0] == 0 and tok[0] == 1
+    picks = set()
+    for _ in range(50):
+        u = float(torch.rand((), generator=g))
+        tok, st = sample_arrays(x, [1.0], [2], [1.0], [u])
+        picks.add(int(tok[0]))
+    assert picks <= {1, 3} and len(picks) == 2
+
+
+def test_edge_values(dev):
+    nan, inf = float("nan"), float("inf")
+    rows = [
+        [1.0, nan, 3.0, nan],          # greedy -> first NaN; stochastic -> NaN status
+        [-inf, -inf, -inf, -inf],      # greedy -> 0; stochastic -> nonfinite
+        [-0.0, 0.0, -0.0, 0.0],        # -0 and +0 tie
+        [inf, 1.0, 2.0, 3.0],          # greedy -> 0; stochastic -> nonfinite
+        [-inf, 2.0, -inf, 2.0],        # -inf entries get zero mass
+        [3e38, 3.3e38, -3e38, 0.0],    # overflow after /T for small T
+    ]
+    base = torch.tensor(rows, dtype=torch.float32)
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        logits = base.to(dtype)
+        n = logits.shape[0]
+        for T in (0.0, 1.0, 0.5):
+            run_case(dev, f"edge_{DT_NAME[dtype]}_T{T}", logits, [T] * n, [0] * n, [1.0] * n, [0.3] * n)
+        run_case(dev, f"edge_{DT_NAME[dtype]}_topk", logits, [1.0] * n, [2] * n, [0.7] * n, [0.6] * n)
+
+
+def test_row_map_and_unaligned(dev):
+    g = torch.Generator().manual_seed(5)
+    big = torch.randn(6, 1003, generator=g)
+    # a strided view with an odd row stride exercises the element-load path
+    view = big[:, :1000]
+    rm = [5, 0, 0, 3, 2, 5, 1]
+    T = [1.0, 0.0, 0.8, 1.2, 1.0, 0.5, 1.0]
+    K = [0, 0, 10, 0, 3, 0, 100]
+    P = [0.9, 1.0, 1.0, 0.5, 1.0, 0.99, 0.8]
+    U = [0.1, 0.0, 0.5, 0.9, 0.2, 0.7, 0.33]
+    x = big.to(dev)[:, :1000]
+    assert x.stride(0) == 1003
+    out = sample_arrays(x, T, K, P, U, row_map=rm, debug=True)
+    refs = oracle.sample_batch(view.contiguous().numpy(), "float32", T, K, P, U, row_map=rm, want_probs=True)
+    rep = compare_rows(out.tokens, out.status, refs, [t == 0 for t in T], probs=out.probs.cpu().numpy(),
+                       kept=out.kept.cpu().numpy(), info=out.info)
+    assert rep.ok(), rep.summary()
+    bad = sample_arrays(x, [1.0], [0], [1.0], [0.5], row_map=[6])
+    assert bad[1][0] == oracle.ROW_BAD_PARAM
+
+
+def test_mixed256_llama3_bf16(dev):
+    w = workloads.mixed256_llama3_bf16()
+    run_case(dev, w.name, w.logits, w.temperature, w.top_k, w.top_p, w.uniform)
+
+
+def test_nucleus_qwen_fp32_subset(dev):
+    # the full 1024 x 151936 workload through row_map on 12 rows (the oracle sorts each row)
+    w = workloads.nucleus1024_qwen_fp32(rows=16)
+    rm = list(range(12))
+    run_case(dev, w.name + "_subset", w.logits, w.temperature[:12], w.top_k[:12], w.top_p[:12], w.uniform[:12],
+             row_map=rm)
