@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""Sampler benchmark: sampled rows/s and HBM roofline on one MI355X.
+
+One step = one engine step's sampling: a single ``pbs_sample`` launch over all rows of
+the ``mixed256_llama3_bf16`` workload (bf16 logits [256, 128256], mixed temperature /
+top-k / top-p per row). Inputs are resident in HBM before timing; the step rotates over
+several copies of the logits (> 256 MB in total) so the 256 MB Infinity Cache cannot
+serve a step from the previous one. Per-row parameters and uniforms live on the device,
+so the timed region is the kernel plus launch only.
+
+Prints one JSON line (rank 0): metric/value/unit as BASELINE.json names them, plus a
+``roofline`` object for the sampling kernel and a ``cpu_baseline`` object (the op-for-op
+CPU restatement of pagedbatch/sampling.py timed on this host in the same run).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+METRIC = "sampled rows/s + HBM GB/s (% peak), bf16 logits 256×128256 mixed top-k/p"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="mixed256_llama3_bf16",
+                    choices=["mixed256_llama3_bf16", "greedy512_quantized", "nucleus1024_qwen_fp32",
+                             "steps8_smollm_mixed"])
+    ap.add_argument("--copies", type=int, default=0, help="logits copies to rotate over (default: > 256 MB)")
+    ap.add_argument("--cpu-steps", type=int, default=3, help="CPU baseline steps (median)")
+    ap.add_argument("--cpu-rows", type=int, default=0, help="CPU baseline rows per step (0: all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-parity", action="store_true", help="skip the token check against the oracle")
+    return ap.parse_args()
+
+
+def cpu_baseline(w, steps: int, rows: int):
+    """Time the op-for-op CPU restatement of sampling.py (engine.py:133-139 row loop)."""
+    import torch
+
+    from oracle.reference_ops import engine_step_ops
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    n = rows or w.rows
+    logits = w.logits[:n].contiguous()
+    params = [(w.temperature[i], w.top_k[i], w.top_p[i]) for i in range(n)]
+    times = []
+    for s in range(steps):
+        gens = [torch.Generator().manual_seed(1000 * s + i) for i in range(n)]
+        t0 = time.perf_counter()
+        engine_step_ops(logits, params, gens)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(n / med, 3),
+        "unit": "rows/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{n} of {w.rows} rows of {w.name}, median of {steps} steps "
+                  f"({med * 1e3:.1f} ms/step, {med / n * 1e3:.2f} ms/row), torch {torch.__version__} CPU",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build samples on a single device and has no "
+              f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from pagedbatch_amd import _lib, workloads
+    from pagedbatch_amd.sampling import _TORCH_DTYPE
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    print(f"[bench] building workload {args.workload}", file=sys.stderr, flush=True)
+    w = workloads.WORKLOADS[args.workload]()
+    rows, vocab = w.rows, w.vocab
+    elt = w.logits.element_size()
+    alg_bytes = rows * vocab * elt
+    copies = args.copies or max(2, -(-300_000_000 // alg_bytes))
+    bufs = [w.logits.to(dev) for _ in range(copies)]
+    T = torch.tensor(w.temperature, dtype=torch.float32, device=dev)
+    K = torch.tensor([k if 0 < k < vocab else 0 for k in w.top_k], dtype=torch.int32, device=dev)
+    P = torch.tensor(w.top_p, dtype=torch.float32, device=dev)
+    U = torch.tensor(w.uniform, dtype=torch.float32, device=dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    dcode = _TORCH_DTYPE[w.logits.dtype]
+    stream = torch.cuda.current_stream(dev)
+
+    def launch(i):
+        x = bufs[i % copies]
+        rc = lib.pbs_sample(x.data_ptr(), dcode, rows, rows, vocab, vocab, None, T.data_ptr(), K.data_ptr(),
+                            P.data_ptr(), U.data_ptr(), tok.data_ptr(), st.data_ptr(), None, 0, stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"pbs_sample failed: {_lib.last_error(lib)}")
+
+    print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+
+    # per-launch kernel durations (events on the stream the kernel runs on)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g0 = torch.cuda.Event(enable_timing=True)
+    g1 = torch.cuda.Event(enable_timing=True)
+    g0.record(stream)
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        launch(i)
+        ev[i][1].record(stream)
+    g1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_total_ms = g0.elapsed_time(g1)
+    per_launch_ms = [a.elapsed_time(b) for a, b in ev]
+    kern_ms = statistics.mean(per_launch_ms)
+    step_ms = max(wall * 1e3, gpu_total_ms) / args.steps
+    value = rows / (step_ms / 1e3)
+    achieved = alg_bytes / (kern_ms / 1e3) / 1e9
+
+    status = st.cpu().numpy()
+    tokens = tok.cpu().numpy()
+    parity = None
+    if not args.no_parity:
+        from oracle import oracle
+        from oracle.compare import compare_rows
+
+        n = min(rows, 64)
+        raw = w.logits[:n]
+        raw = raw.view(torch.int16).numpy().view(np.uint16) if raw.dtype == torch.bfloat16 else raw.numpy()
+        dt = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}[w.logits.dtype]
+        refs = oracle.sample_batch(raw, dt, w.temperature[:n], w.top_k[:n], w.top_p[:n], w.uniform[:n])
+        rep = compare_rows(tokens[:n], status[:n], refs, [t == 0 for t in w.temperature[:n]])
+        parity = {"rows": n, "ok": rep.ok(), "tokens_checked": rep.checked_tokens, "exempt": rep.exempt_tokens}
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(w, args.cpu_steps, args.cpu_rows)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "us_per_step_kernel": round(kern_ms * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w.logits.dtype],
+        "data": "synthetic (seeded logits recipe, see pagedbatch_amd/workloads.py)",
+        "config": {"workload": w.name, "rows": rows, "vocab": vocab, "logits_dtype": str(w.logits.dtype),
+                   "buffers_rotated": copies, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": alg_bytes},
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
+        "parity": parity,
+        "row_status_ok": bool((status == 0).all()),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -125,8 +125,9 @@ int pbs_sample(const void* logits, int dtype, int64_t n_logit_rows, int64_t rows
  * pbs_sample plus diagnostics for parity tests: out_probs (device
  * float[rows*vocab], the final softmax over the kept set, 0 elsewhere; may be
  * NULL), out_kept (device uint8[rows*vocab], 1 for kept tokens; may be NULL)
- * and out_info (device pbs_row_info[rows]; may be NULL). Tokens and statuses
- * are identical to pbs_sample's for the same inputs.
+ * and out_info (device pbs_row_info[rows]; may be NULL unless out_probs or
+ * out_kept is requested). Greedy rows report probability 1 on their token.
+ * Tokens and statuses are identical to pbs_sample's for the same inputs.
  */
 int pbs_sample_debug(const void* logits, int dtype, int64_t n_logit_rows, int64_t rows, int64_t vocab,
                      int64_t row_stride, const int32_t* row_map, const float* temperature,
