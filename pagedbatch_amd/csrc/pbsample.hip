@@ -36,6 +36,7 @@ constexpr int NT = 1024;           // threads per workgroup: one workgroup per r
 constexpr int NWAVE = NT / 64;     // wave64
 constexpr int HIST_WORDS = 32768;  // 64K packed u16 counters = 128 KB of LDS
 constexpr int NGROUP = 256;        // histogram groups of 256 ords (high byte of a 16-bit ord)
+constexpr int PARK_CHUNKS = 16;    // register-row chunks wave 0 can park in LDS
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -176,6 +177,17 @@ __device__ __forceinline__ double exp_neg(double d) {
   q = fma(q, r, 1.0);
   q = fma(q, r, 1.0);
   return ldexp(q, (int)n);
+}
+
+// exp(x - m) for fp32 x <= m: the difference and its scaling by log2(e) in fp64, the
+// fractional power of two (|f| <= 1/2) on the hardware exp2, the integer power exact.
+// Relative error about 1.5e-7; deterministic.
+__device__ __forceinline__ double weight_f(float x, float m) {
+  if (!(x > -INFINITY)) return 0.0;
+  double t = ((double)x - (double)m) * 1.4426950408889634074;
+  t = fmax(t, -1100.0);
+  const double n = rint(t);
+  return ldexp((double)__builtin_amdgcn_exp2f((float)(t - n)), (int)n);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -348,6 +360,9 @@ struct __align__(16) Smem {
   uint32_t gabove_cnt[NGROUP];   // count strictly above the group (descending order)
   double gmass[NGROUP];          // fp64 mass of each group
   double gabove_mass[NGROUP];    // mass strictly above the group
+  u4 park[PARK_CHUNKS * 64];     // wave 0's register row slice while it runs resolve16
+  uint32_t gc_n[256];            // bins of the group a 16-bit search is in: counts
+  double gc_w[256];              // and masses, by bin offset inside the group
   double red_d[NWAVE];
   float red_f[NWAVE];
   int red_i[2 * NWAVE];
@@ -462,14 +477,16 @@ struct RegRow {
     nvec = nvec_;
     vocab = vocab_;
   }
-  // Unconditional loads of a clamped address keep the code straight-line, so the
-  // compiler waits for each chunk only when it is first used.
+  // Raw buffer loads: one VGPR offset (the thread's) for every chunk, the chunk offset in
+  // an SGPR, and the buffer's range check returning zeros past the row end, so the code
+  // stays straight-line and the compiler waits for each chunk only when it is first used.
+  // Non-temporal: the row is read exactly once.
   __device__ __forceinline__ void load() {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, nvec * 16, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int v = j * NT + (int)threadIdx.x;
-      r[j] = __builtin_nontemporal_load(row + (v < nvec ? v : nvec - 1));
-    }
+    for (int j = 0; j < NCH; ++j)
+      r[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, j * NT * 16, 2));
   }
   // f(j, q, base_index, valid): q is the 16-byte vector, base_index its first element
   template <class F>
@@ -635,35 +652,57 @@ __device__ __forceinline__ int select_index(const Src& src, Smem& s, M&& match, 
   return r;
 }
 
-// Index selection for register-resident rows. The per-(chunk, wave) match counts come
-// from ballots of the per-element compares (scalar popcounts, skipped for chunks where the
-// wave has no match), so the pass costs one compare per element; only the wave holding
-// the answer then looks at lanes.
-template <int DT, int NCH, class M>
-__device__ __forceinline__ int select_index_reg(const RegRow<DT, NCH>& src, Smem& s, M&& match, int rank) {
-  constexpr int EPV = DTraits<DT>::EPV;
+// Index selection for register-resident 16-bit rows: the rank-th lowest-index element
+// whose (unfolded) ord lies in [lo, lo + span]. Per-(chunk, wave) match counts come from
+// ballots of the per-element compares (scalar popcounts, skipped where the wave has no
+// match in the chunk), so the pass costs about two VALU ops per element; only the wave
+// holding the answer then looks at its lanes.
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+template <int DT, int NCH>
+__device__ __forceinline__ uint32_t match_bits16(const RegRow<DT, NCH>& src, int j, uint32_t lo2, uint32_t span) {
+  uint32_t bits = 0;
+  if (j * NT + (int)threadIdx.x < src.nvec) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t dl = pk_sub_u16(ord16_pair(src.r[j][d]), lo2);
+      bits |= ((dl & 0xffffu) <= span ? 1u : 0u) << (2 * d);
+      bits |= ((dl >> 16) <= span ? 1u : 0u) << (2 * d + 1);
+    }
+  }
+  return bits;
+}
+
+template <int DT, int NCH>
+__device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Smem& s, uint32_t lo, uint32_t span,
+                                                  int rank) {
   static_assert(NCH * NWAVE <= 256, "chunk table must fit 4 entries per lane");
   const int l = lane_id(), w = wave_id();
+  const uint32_t lo2 = lo | (lo << 16);
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const bool vv = j * NT + (int)threadIdx.x < src.nvec;
-    uint64_t mk[EPV];
+    uint64_t mk[8];
     uint64_t any = 0;
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      mk[e] = ballot(vv && match(elem_raw<DT>(src.r[j], e)));
-      any |= mk[e];
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t dl = pk_sub_u16(ord16_pair(src.r[j][d]), lo2);
+      mk[2 * d] = ballot(vv && (dl & 0xffffu) <= span);
+      mk[2 * d + 1] = ballot(vv && (dl >> 16) <= span);
+      any |= mk[2 * d] | mk[2 * d + 1];
     }
     uint32_t c = 0;
     if (any) {
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) c += (uint32_t)__popcll(mk[e]);
+      for (int e = 0; e < 8; ++e) c += (uint32_t)__popcll(mk[e]);
     }
     if (l == 0) s.hist[j * NWAVE + w] = c;
+    __builtin_amdgcn_sched_barrier(0);  // one chunk's masks live at a time
   }
   __syncthreads();
   if (w == 0) {
-    // positions p = j*NWAVE + wave, in index order; lane l holds p = 4l .. 4l+3
+    // positions p = j*NWAVE + wave are in index order; lane l holds p = 4l .. 4l+3
     uint32_t c[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) c[i] = (4 * l + i < NCH * NWAVE) ? s.hist[4 * l + i] : 0u;
@@ -696,47 +735,23 @@ __device__ __forceinline__ int select_index_reg(const RegRow<DT, NCH>& src, Smem
   }
   __syncthreads();
   const int pos = s.sel_jstar;
-  if (pos < 0) {
-    __syncthreads();
-    return -1;
-  }
-  const int jstar = pos / NWAVE, wstar = pos % NWAVE, rr = s.sel_rank;
-  if (w == wstar) {
-    uint32_t bits = 0;
+  if (pos >= 0) {
+    const int jstar = pos / NWAVE, wstar = pos % NWAVE, rr = s.sel_rank;
+    if (w == wstar) {
+      uint32_t bits = 0;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      if (j == jstar) {
-        const bool vv = j * NT + (int)threadIdx.x < src.nvec;
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) bits |= (vv && match(elem_raw<DT>(src.r[j], e))) ? (1u << e) : 0u;
+      for (int j = 0; j < NCH; ++j)
+        if (j == jstar) bits = match_bits16(src, j, lo2, span);
+      const uint32_t cnt = (uint32_t)__popc(bits);
+      const uint32_t incl = wscan_u32(cnt);
+      const uint32_t excl = incl - cnt;
+      if ((uint32_t)rr >= excl && (uint32_t)rr < incl) {
+        uint32_t b = bits;
+        for (uint32_t k = (uint32_t)rr - excl; k > 0; --k) b &= b - 1u;
+        s.sel_index = (jstar * NT + (int)threadIdx.x) * 8 + (__ffs(b) - 1);
       }
     }
-    const uint32_t cnt = (uint32_t)__popc(bits);
-    const uint32_t incl = wscan_u32(cnt);
-    const uint32_t excl = incl - cnt;
-    if ((uint32_t)rr >= excl && (uint32_t)rr < incl) {
-      uint32_t b = bits;
-      for (uint32_t k = (uint32_t)rr - excl; k > 0; --k) b &= b - 1u;
-      s.sel_index = (jstar * NT + (int)threadIdx.x) * EPV + (__ffs(b) - 1);
-    }
   }
-  __syncthreads();
-  const int r = s.sel_index;
-  __syncthreads();
-  return r;
-}
-
-// the only element whose raw bits satisfy `match` (the caller knows there is exactly one)
-template <int DT, class Src, class M>
-__device__ __forceinline__ int locate_unique(const Src& src, Smem& s, M&& match) {
-  constexpr int EPV = DTraits<DT>::EPV;
-  if (threadIdx.x == 0) s.sel_index = -1;
-  __syncthreads();
-  src.for_each([&](int, const u4& q, int base, bool vvalid) {
-#pragma unroll
-    for (int e = 0; e < EPV; ++e)
-      if (elem_valid(src, vvalid, base + e) && match(elem_raw<DT>(q, e))) s.sel_index = base + e;
-  });
   __syncthreads();
   const int r = s.sel_index;
   __syncthreads();
@@ -786,90 +801,105 @@ __device__ __forceinline__ float scaled16(uint32_t o, float T) {
 // the exact fp32 scaled value (pagedbatch takes softmax of the fp32 scaled row, sampling.py:26)
 template <int DT>
 __device__ __forceinline__ double weight16(uint32_t o, float T, float m) {
-  return exp_neg((double)scaled16<DT>(o, T) - (double)m);
+  return weight_f(scaled16<DT>(o, T), m);
 }
 
-// One group's 256 bins as seen by a wave, restricted to ords >= lo: lane l holds the bins
-// at descending positions 4l..4l+3 (ords g*256+255-4l-i), their counts and masses.
+// The bins of one group, cached in LDS by wave 0 for the searches of resolve16: counts
+// and masses by bin offset. Lane l works on the bins at descending positions 4l..4l+3,
+// i.e. offsets 255-4l-i.
 template <int DT>
-struct GroupScan {
-  uint32_t g;
+__device__ __forceinline__ void load_group(Smem& s, uint32_t g, float T, float m) {
+  const int l = lane_id();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = (uint32_t)(4 * l + i);
+    const uint32_t n = hist_count(s, g * 256u + off);
+    s.gc_n[off] = n;
+    s.gc_w[off] = n ? (double)n * weight16<DT>(g * 256u + off, T, m) : 0.0;
+  }
+}
+
+// count and mass of the cached group's bins with ord >= t
+__device__ __forceinline__ void group_ge(const Smem& s, uint32_t g, uint32_t t, uint32_t& cnt, double& mass) {
+  const int l = lane_id();
+  uint32_t c = 0;
+  double ms = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = (uint32_t)(4 * l + i);
+    if (g * 256u + off >= t) {
+      c += s.gc_n[off];
+      ms += s.gc_w[off];
+    }
+  }
+  cnt = wsum_u32(c);
+  mass = wsum_f64(ms);
+}
+
+// first ord >= lo of the cached group (descending) whose inclusive count from the top of
+// the group reaches need
+__device__ __forceinline__ uint32_t group_find_count(const Smem& s, uint32_t g, uint32_t lo, uint32_t need) {
+  const int l = lane_id();
   uint32_t n[4];
-  double w[4];  // mass of each bin (count * weight)
-  __device__ __forceinline__ void load(const Smem& s, uint32_t g_, uint32_t lo, float T, float m, bool want_mass) {
-    g = g_;
-    const int l = lane_id();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t o = g * 256u + 255u - (uint32_t)(4 * l + i);
-      n[i] = (o >= lo) ? hist_count(s, o) : 0u;
-      w[i] = (want_mass && n[i]) ? (double)n[i] * weight16<DT>(o, T, m) : 0.0;
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = 255u - (uint32_t)(4 * l + i);
+    n[i] = (g * 256u + off >= lo) ? s.gc_n[off] : 0u;
+  }
+  const uint32_t tot = n[0] + n[1] + n[2] + n[3];
+  const uint32_t incl = wscan_u32(tot);
+  const uint64_t hit = ballot(incl >= need);
+  const int L = hit ? first_lane(hit) : 63;
+  uint32_t run = incl - tot;
+  int found = 3;
+  bool done = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (!done && run + n[i] >= need) {
+      found = i;
+      done = true;
     }
+    run += n[i];
   }
-  __device__ __forceinline__ uint32_t ord(int l, int i) const { return g * 256u + 255u - (uint32_t)(4 * l + i); }
-  // count / mass of the group's bins with ord >= t
-  __device__ __forceinline__ uint32_t count_ge(uint32_t t) const {
-    const int l = lane_id();
-    uint32_t c = 0;
+  return g * 256u + 255u - bcast_u32((uint32_t)(4 * l + found), L);
+}
+
+// first ord >= lo of the cached group (descending) whose inclusive mass, starting from
+// `base` above the group, exceeds target; the lowest non-empty ord >= lo if rounding keeps
+// the cumulative at or below the target
+__device__ __forceinline__ uint32_t group_find_mass(const Smem& s, uint32_t g, uint32_t lo, double base,
+                                                    double target) {
+  const int l = lane_id();
+  double w[4];
+  uint32_t any = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c += (ord(l, i) >= t) ? n[i] : 0u;
-    return wsum_u32(c);
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = 255u - (uint32_t)(4 * l + i);
+    const bool in = g * 256u + off >= lo;
+    w[i] = in ? s.gc_w[off] : 0.0;
+    any |= (in && s.gc_n[off]) ? (1u << i) : 0u;
   }
-  __device__ __forceinline__ double mass_ge(uint32_t t) const {
-    const int l = lane_id();
-    double c = 0.0;
+  const double tot = w[0] + w[1] + w[2] + w[3];
+  const double incl = wscan_f64(tot);
+  double excl = __shfl_up(incl, 1);
+  if (l == 0) excl = 0.0;
+  uint64_t hit = ballot(base + incl > target);
+  bool last = false;
+  if (!hit) {
+    hit = ballot(any != 0u);
+    last = true;
+  }
+  const int L = last ? 63 - __clzll((unsigned long long)hit) : first_lane(hit);
+  double run = base + excl;
+  int found = -1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c += (ord(l, i) >= t) ? w[i] : 0.0;
-    return wsum_f64(c);
+  for (int i = 0; i < 4; ++i) {
+    const bool take = last ? ((any >> i) & 1u) != 0u : (found < 0 && run + w[i] > target);
+    if (take) found = i;
+    run += w[i];
   }
-  // first ord (descending) whose inclusive count from the top of the group reaches need
-  __device__ __forceinline__ uint32_t find_count(uint32_t need) const {
-    const int l = lane_id();
-    const uint32_t tot = n[0] + n[1] + n[2] + n[3];
-    const uint32_t incl = wscan_u32(tot);
-    const uint64_t hit = ballot(incl >= need);
-    const int L = hit ? first_lane(hit) : 63;
-    uint32_t run = incl - tot;
-    int found = -1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (found < 0 && run + n[i] >= need) found = i;
-      run += n[i];
-    }
-    return bcast_u32(ord(l, found < 0 ? 3 : found), L);
-  }
-  // first ord (descending) whose inclusive mass, starting from `base` above the group,
-  // exceeds target; the lowest non-empty ord if rounding keeps it at or below the target.
-  // `above` gets the cumulative mass strictly above the returned ord.
-  __device__ __forceinline__ uint32_t find_mass(double base, double target, double& above) const {
-    const int l = lane_id();
-    const double tot = w[0] + w[1] + w[2] + w[3];
-    const double incl = wscan_f64(tot);
-    double excl = __shfl_up(incl, 1);
-    if (l == 0) excl = 0.0;
-    uint64_t hit = ballot(base + incl > target);
-    bool last = false;
-    if (!hit) {
-      hit = ballot(n[0] + n[1] + n[2] + n[3] > 0u);
-      last = true;
-    }
-    const int L = last ? 63 - __clzll((unsigned long long)hit) : first_lane(hit);
-    double run = base + excl;
-    int found = -1;
-    double ab = 0.0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool take = last ? (n[i] > 0u) : (found < 0 && run + w[i] > target);
-      if (take) {
-        found = i;
-        ab = run;
-      }
-      run += w[i];
-    }
-    above = bcast_f64(ab, L);
-    return bcast_u32(ord(l, found < 0 ? 3 : found), L);
-  }
-};
+  return g * 256u + 255u - bcast_u32((uint32_t)(4 * l + (found < 0 ? 3 : found)), L);
+}
 
 // Ords whose scaled value equals that of ord o. Distinct 16-bit values only meet after the
 // division by T at the under/overflow ends; the map is monotone, so binary search.
@@ -899,8 +929,8 @@ __device__ __forceinline__ void tie_range16(uint32_t o, float T, uint32_t& lo, u
   hi = a;
 }
 
-// the group holding the need-th element (descending), over ords >= lo whose partial lowest
-// group has count cnt_lo; -1 if fewer elements
+// The group holding the need-th element (descending) of ords >= lo, whose partial lowest
+// group holds cnt_lo; -1 if fewer elements.
 __device__ __forceinline__ int find_group_count(const Smem& s, uint32_t lo, uint32_t cnt_lo, uint32_t need) {
   const int l = lane_id();
   const uint32_t glo = lo >> 8;
@@ -916,10 +946,11 @@ __device__ __forceinline__ int find_group_count(const Smem& s, uint32_t lo, uint
   return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
 }
 
-// the group whose cumulative mass interval [above, above + mass) holds target, over ords
-// >= lo whose partial lowest group has mass mass_lo. Groups tile the cumulative exactly
+// The group whose cumulative mass interval [above, above + mass) holds target, over ords
+// >= lo whose partial lowest group holds mass_lo. Groups tile the cumulative exactly
 // because each group's upper end is the next lower group's stored "above".
-__device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, double mass_lo, double total, double target) {
+__device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, double mass_lo, double total,
+                                                         double target) {
   const int l = lane_id();
   const uint32_t glo = lo >> 8;
   int found = -1;
@@ -936,194 +967,162 @@ __device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, doubl
   return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
 }
 
-// count / mass of ords >= t (t inside the histogram range)
-template <int DT>
-__device__ __forceinline__ uint32_t count_ge(const Smem& s, uint32_t t, float T, float m) {
-  GroupScan<DT> gs;
-  gs.load(s, t >> 8, t, T, m, false);
-  return s.gabove_cnt[t >> 8] + gs.count_ge(t);
-}
-template <int DT>
-__device__ __forceinline__ double mass_ge(const Smem& s, uint32_t t, float T, float m) {
-  GroupScan<DT> gs;
-  gs.load(s, t >> 8, t, T, m, true);
-  return s.gabove_mass[t >> 8] + gs.mass_ge(t);
+// Index of the rank-th lowest-index element whose ord lies in [lo, hi] (-0 counts as +0).
+template <int DT, class Src>
+__device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank) {
+  // -0 carries ord 0x7fff in the unfolded pair encoding and belongs with +0 (0x8000)
+  const uint32_t lo_u = (lo == 0x8000u) ? 0x7fffu : lo;
+  const uint32_t span = hi - lo_u;
+  if constexpr (Src::kStore) {
+    return select_index_reg16(src, s, lo_u, span, rank);
+  } else {
+    return select_index<DT>(src, s, [=](uint32_t raw) { return (ord16_pair(raw) & 0xffffu) - lo_u <= span; }, rank);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
 // 16-bit stochastic row
 // ---------------------------------------------------------------------------------------
 
-// Index of the rank-th lowest-index element whose ord lies in [lo, hi]. A single ord (the
-// usual case) is matched on its raw bits: both zero encodings for the +0 ord.
-template <int DT, class Src>
-__device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank) {
-  if (lo == hi) {
-    const uint32_t r0 = raw_of_ord16(lo);
-    const uint32_t r1 = (r0 == 0u) ? 0x8000u : r0;
-    auto eq = [=](uint32_t raw) { return raw == r0 || raw == r1; };
-    if constexpr (Src::kStore) {
-      return select_index_reg(src, s, eq, rank);
-    } else {
-      return select_index<DT>(src, s, eq, rank);
-    }
-  }
-  auto in = [=](uint32_t raw) {
-    const uint32_t o = ord16(raw);
-    return o >= lo && o <= hi;
-  };
-  if constexpr (Src::kStore) {
-    return select_index_reg(src, s, in, rank);
-  } else {
-    return select_index<DT>(src, s, in, rank);
-  }
-}
-
 // Top-k threshold, top-p cutoff and draw position from the histogram summaries. Runs on
-// wave 0 only and leaves the result in s.st.
+// wave 0 only and leaves the result in s.st. The three searches share one loop body (one
+// copy of the code in the instruction cache); the bins of the group being searched are
+// cached in LDS, which keeps the loop's register footprint small.
 template <int DT>
 __device__ __forceinline__ void resolve16(Smem& s, int V, float T, int kk, float p, float u, float m) {
-  RowState st = {};
-  st.status = PBS_ROW_OK;
-  st.m = m;
-  st.x_kth = -INFINITY;
+  const int l = lane_id();
+  RowState& st = s.st;  // written by lane 0
+  if (l == 0) {
+    st = RowState{};
+    st.status = PBS_ROW_OK;
+    st.m = m;
+    st.x_kth = -INFINITY;
+  }
   const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
   const double total_mass = s.gabove_mass[0] + s.gmass[0];
   // a u16 counter wraps only if one value occurs more than 65535 times
   if (total_cnt != (uint32_t)V) {
-    st.status = -1;
-    if (lane_id() == 0) s.st = st;
+    if (l == 0) st.status = -1;
     return;
   }
-
-  // top-k (sampling.py:15-17): K = ords >= kord_lo
-  uint32_t kord_lo = 0u;
-  if (kk > 0 && kk < V) {
-    const int g = find_group_count(s, 0u, s.gcount[0], (uint32_t)kk);
-    GroupScan<DT> gs;
-    gs.load(s, (uint32_t)g, 0u, T, m, false);
-    const uint32_t o = gs.find_count((uint32_t)kk - s.gabove_cnt[g]);
-    uint32_t lo, hi;
-    tie_range16<DT>(o, T, lo, hi);
-    kord_lo = lo;
-    st.x_kth = scaled16<DT>(o, T);
-  }
-  st.kord_lo = kord_lo;
-  const uint32_t glo = kord_lo >> 8;
-  GroupScan<DT> gk;
-  gk.load(s, glo, kord_lo, T, m, true);
-  const uint32_t cnt_lo = gk.count_ge(kord_lo);
-  const double mass_lo = gk.mass_ge(kord_lo);
-  const uint32_t nk = s.gabove_cnt[glo] + cnt_lo;
-  const double zk = (kord_lo == 0u) ? total_mass : s.gabove_mass[glo] + mass_lo;
-  st.zk = zk;
-
-  // top-p (sampling.py:18-25): the shortest prefix (value desc, index asc) whose
-  // exclusive mass is <= p*Z; inside the cutoff tie group the lowest indices survive
-  bool have_cut = false;
-  double above_cut = 0.0;
-  if (p < 1.0f) {
-    const double tau = (double)p * zk;
-    const int g = find_group_mass(s, kord_lo, mass_lo, total_mass, tau);
-    if (g >= 0) {
-      GroupScan<DT> gs;
-      gs.load(s, (uint32_t)g, kord_lo, T, m, true);
-      double ab;
-      const uint32_t o = gs.find_mass(s.gabove_mass[g], tau, ab);
-      uint32_t lo, hi;
-      tie_range16<DT>(o, T, lo, hi);
-      lo = max(lo, kord_lo);
-      double B;
-      uint32_t n_above, n_ge;
-      if (lo == o && hi == o) {
-        B = ab;
-        n_ge = s.gabove_cnt[g] + gs.count_ge(o);
-        n_above = n_ge - hist_count(s, o);
-      } else {
-        B = mass_ge<DT>(s, hi + 1u, T, m);
-        n_above = count_ge<DT>(s, hi + 1u, T, m);
-        n_ge = count_ge<DT>(s, lo, T, m);
+  uint32_t cached = 0xffffffffu;
+  uint32_t kord_lo = 0u, nk = (uint32_t)V, cut_hi = 0u;
+  double zk = total_mass, B_cut = 0.0, t = 0.0;
+#pragma unroll 1
+  for (int q = 0; q < 3; ++q) {
+    // q = 0: k-th largest (count k over all ords); q = 1: top-p cutoff (mass p*Z over K) or
+    // the lowest value of K (count |K|); q = 2: draw point (mass u*Z_P above the cutoff group)
+    bool by_mass = false;
+    uint32_t lo = 0u, need = 0u;
+    double target = 0.0;
+    if (q == 0) {
+      if (!(kk > 0 && kk < V)) continue;
+      need = (uint32_t)kk;
+    } else if (q == 1) {
+      lo = kord_lo;
+      by_mass = p < 1.0f;
+      target = (double)p * zk;
+      need = nk;
+    } else {
+      if (!(t < B_cut)) break;
+      lo = cut_hi + 1u;
+      by_mass = true;
+      target = t;
+    }
+    // the partial lowest group of the range, then the group the search lands in
+    const uint32_t glo = lo >> 8;
+    if (cached != glo) {
+      load_group<DT>(s, glo, T, m);
+      cached = glo;
+    }
+    uint32_t cnt_lo;
+    double mass_lo;
+    group_ge(s, glo, lo, cnt_lo, mass_lo);
+    int g = -1;
+    if (by_mass) g = find_group_mass(s, lo, mass_lo, total_mass, target);
+    if (g < 0 && (q == 1 || !by_mass)) {
+      by_mass = false;  // q = 1 with p*Z reaching all of K: the cutoff group is K's lowest value
+      g = find_group_count(s, lo, cnt_lo, need);
+    }
+    if (g < 0) break;
+    if (cached != (uint32_t)g) {
+      load_group<DT>(s, (uint32_t)g, T, m);
+      cached = (uint32_t)g;
+    }
+    const uint32_t o = by_mass ? group_find_mass(s, (uint32_t)g, lo, s.gabove_mass[g], target)
+                               : group_find_count(s, (uint32_t)g, lo, need - s.gabove_cnt[g]);
+    uint32_t tlo, thi;
+    tie_range16<DT>(o, T, tlo, thi);
+    tlo = max(tlo, lo);
+    // count and mass above each end of the tie group
+    uint32_t n_above = 0u, n_ge = 0u;
+    double B = 0.0, mass_ge_lo = 0.0;
+#pragma unroll 1
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t tt = (k == 0) ? thi + 1u : tlo;
+      uint32_t c = 0u;
+      double ms = 0.0;
+      if (tt <= 0xffffu) {
+        const uint32_t gg = tt >> 8;
+        if (cached != gg) {
+          load_group<DT>(s, gg, T, m);
+          cached = gg;
+        }
+        group_ge(s, gg, tt, c, ms);
+        c += s.gabove_cnt[gg];
+        ms += s.gabove_mass[gg];
       }
-      st.cut_lo = lo;
-      st.cut_hi = hi;
-      st.n_cut_tie = (int)(n_ge - n_above);
-      const double w = weight16<DT>(o, T, m);
-      double kf = (w > 0.0) ? floor((tau - B) / w) + 1.0 : (double)st.n_cut_tie;
-      kf = fmax(1.0, fmin(kf, (double)st.n_cut_tie));
-      st.n_cut_keep = (int)kf;
-      st.zp = B + (double)st.n_cut_keep * w;
-      st.n_kept = (int)n_above + st.n_cut_keep;
-      st.x_cut = scaled16<DT>(o, T);
-      above_cut = B;
-      have_cut = true;
+      if (k == 0) {
+        n_above = c;
+        B = ms;
+      } else {
+        n_ge = c;
+        mass_ge_lo = ms;
+      }
+    }
+    const int n_tie = (int)(n_ge - n_above);
+    const double w = weight16<DT>(o, T, m);
+    if (q == 0) {
+      kord_lo = tlo;
+      nk = n_ge;
+      zk = mass_ge_lo;
+      if (l == 0) st.x_kth = scaled16<DT>(o, T);
+    } else if (q == 1) {
+      int n_keep = n_tie;
+      double zp = zk;
+      if (by_mass) {
+        double kf = (w > 0.0) ? floor((target - B) / w) + 1.0 : (double)n_tie;
+        n_keep = (int)fmax(1.0, fmin(kf, (double)n_tie));
+        zp = B + (double)n_keep * w;
+      }
+      // draw (sampling.py:26-27, inverse-CDF form): the first kept element whose
+      // cumulative mass exceeds u * Z_P; it lies in the cutoff group unless t < B
+      cut_hi = thi;
+      B_cut = B;
+      t = (double)u * zp;
+      if (l == 0) {
+        st.zk = zk;
+        st.cut_lo = tlo;
+        st.cut_hi = thi;
+        st.n_cut_tie = n_tie;
+        st.n_cut_keep = n_keep;
+        st.x_cut = scaled16<DT>(o, T);
+        st.zp = zp;
+        st.n_kept = by_mass ? (int)n_above + n_keep : (int)nk;
+        st.target = t;
+        st.sel_lo = tlo;
+        st.sel_hi = thi;
+        st.sel_n = n_keep;
+        st.sel_rank = (int)fmax(0.0, fmin((w > 0.0) ? floor((t - B) / w) : 0.0, (double)(n_keep - 1)));
+      }
+    } else if (l == 0) {
+      st.sel_lo = tlo;
+      st.sel_hi = thi;
+      st.sel_n = n_tie;
+      st.sel_rank = (int)fmax(0.0, fmin((w > 0.0) ? floor((t - B) / w) : 0.0, (double)(n_tie - 1)));
     }
   }
-  if (!have_cut) {
-    // no top-p, or p*Z reaches the whole top-k set: all of K is kept, and K's lowest value
-    // is the cutoff tie group
-    const int g = find_group_count(s, kord_lo, cnt_lo, nk);
-    GroupScan<DT> gs;
-    gs.load(s, (uint32_t)g, kord_lo, T, m, false);
-    const uint32_t o = gs.find_count(nk - s.gabove_cnt[g]);
-    uint32_t lo, hi;
-    tie_range16<DT>(o, T, lo, hi);
-    lo = max(lo, kord_lo);
-    st.cut_lo = lo;
-    st.cut_hi = hi;
-    st.n_cut_tie = (lo == o && hi == o) ? (int)hist_count(s, o) : (int)(nk - count_ge<DT>(s, hi + 1u, T, m));
-    st.n_cut_keep = st.n_cut_tie;
-    st.zp = zk;
-    st.n_kept = (int)nk;
-    st.x_cut = scaled16<DT>(o, T);
-    above_cut = (lo == o && hi == o) ? zk - (double)st.n_cut_tie * weight16<DT>(o, T, m) : mass_ge<DT>(s, hi + 1u, T, m);
-  }
-
-  // draw (sampling.py:26-27, inverse-CDF form): the first kept element whose cumulative
-  // mass exceeds u * Z_P
-  const double t = (double)u * st.zp;
-  st.target = t;
-  bool in_cut = true;
-  if (t < above_cut) {
-    const uint32_t plo = st.cut_hi + 1u;
-    GroupScan<DT> gp;
-    gp.load(s, plo >> 8, plo, T, m, true);
-    const double mass_plo = gp.mass_ge(plo);
-    const int g = find_group_mass(s, plo, mass_plo, total_mass, t);
-    if (g >= 0) {
-      GroupScan<DT> gs;
-      gs.load(s, (uint32_t)g, plo, T, m, true);
-      double ab;
-      const uint32_t o = gs.find_mass(s.gabove_mass[g], t, ab);
-      uint32_t lo, hi;
-      tie_range16<DT>(o, T, lo, hi);
-      lo = max(lo, plo);
-      double B;
-      int n;
-      if (lo == o && hi == o) {
-        B = ab;
-        n = (int)hist_count(s, o);
-      } else {
-        B = mass_ge<DT>(s, hi + 1u, T, m);
-        n = (int)(count_ge<DT>(s, lo, T, m) - count_ge<DT>(s, hi + 1u, T, m));
-      }
-      const double w = weight16<DT>(o, T, m);
-      const double rf = (w > 0.0) ? floor((t - B) / w) : 0.0;
-      st.sel_lo = lo;
-      st.sel_hi = hi;
-      st.sel_n = n;
-      st.sel_rank = (int)fmax(0.0, fmin(rf, (double)(n - 1)));
-      in_cut = false;
-    }
-  }
-  if (in_cut) {
-    const double w = weight16<DT>(st.cut_hi, T, m);
-    const double rf = (w > 0.0) ? floor((t - above_cut) / w) : 0.0;
-    st.sel_lo = st.cut_lo;
-    st.sel_hi = st.cut_hi;
-    st.sel_n = st.n_cut_keep;
-    st.sel_rank = (int)fmax(0.0, fmin(rf, (double)(st.n_cut_keep - 1)));
-  }
-  if (lane_id() == 0) s.st = st;
+  if (l == 0) st.kord_lo = kord_lo;
 }
 
 template <int DT, class Src>
@@ -1198,24 +1197,56 @@ __device__ __forceinline__ void sample_row16(const KArgs& a, Smem& s, Src& src, 
   }
   __syncthreads();
 
-  // group summaries, all waves: wave w owns groups w, w+16, ...; empty groups are skipped
-  for (int g = wave_id(); g < NGROUP; g += NWAVE) {
-    const int l = lane_id();
-    const uint32_t w0 = s.hist[g * 128 + 2 * l], w1 = s.hist[g * 128 + 2 * l + 1];
-    uint32_t cnt = 0;
-    double ms = 0.0;
-    if (ballot((w0 | w1) != 0u)) {
+  // group summaries. Counts: thread t sums bins [64t, 64t+64) (a quarter group, eight
+  // 16-byte LDS reads), four lanes make a group. Masses: the
+  // non-empty groups only, ranked and dealt round-robin to the waves; lane l weighs bins
+  // 4l..4l+3 of the group.
+  {
+    const int l = lane_id(), w = wave_id();
+    const u4* h4 = (const u4*)s.hist + threadIdx.x * 8;
+    uint32_t c = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u4 qv = h4[i];
+      const uint32_t q0 = qv.x, q1 = qv.y, q2 = qv.z, q3 = qv.w;
+      c += (q0 & 0xffffu) + (q0 >> 16) + (q1 & 0xffffu) + (q1 >> 16);
+      c += (q2 & 0xffffu) + (q2 >> 16) + (q3 & 0xffffu) + (q3 >> 16);
+    }
+    c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]
+    c += dpp<0x4e>(c, 0u);  // quad_perm [2,3,0,1]
+    if ((l & 3) == 0) s.gcount[threadIdx.x >> 2] = c;
+  }
+  __syncthreads();
+  {
+    const int l = lane_id(), w = wave_id();
+    uint32_t ne = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ne |= (s.gcount[4 * l + i] != 0u ? 1u : 0u) << i;
+    if (w == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!((ne >> i) & 1u)) s.gmass[4 * l + i] = 0.0;
+    }
+    const uint32_t cnt = (uint32_t)__popc(ne);
+    const uint32_t incl = wscan_u32(cnt);
+    const uint32_t excl = incl - cnt;
+    const uint32_t total = bcast_u32(incl, 63);
+#pragma unroll 1
+    for (uint32_t r = (uint32_t)w; r < total; r += NWAVE) {
+      const bool mine = r >= excl && r < incl;
+      const int L = first_lane(ballot(mine));
+      // only the owning lane's rank is meaningful (and bounded by its popcount, <= 4)
+      uint32_t bits = ne;
+      for (uint32_t k = mine ? r - excl : 0u; k > 0u; --k) bits &= bits - 1u;
+      const uint32_t g = bcast_u32(4u * (uint32_t)l + (uint32_t)(__ffs(bits) - 1), L);
+      const uint32_t w0 = s.hist[g * 128u + 2u * l], w1 = s.hist[g * 128u + 2u * l + 1u];
       const uint32_t n[4] = {w0 & 0xffffu, w0 >> 16, w1 & 0xffffu, w1 >> 16};
       double part = 0.0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (n[i]) part += (double)n[i] * weight16<DT>((uint32_t)(g * 256 + 4 * l + i), T, m);
-      cnt = wsum_u32(n[0] + n[1] + n[2] + n[3]);
-      ms = wsum_f64(part);
-    }
-    if (l == 0) {
-      s.gcount[g] = cnt;
-      s.gmass[g] = ms;
+      for (int k = 0; k < 4; ++k)
+        if (n[k]) part += (double)n[k] * weight16<DT>(g * 256u + 4u * l + (uint32_t)k, T, m);
+      part = wsum_f64(part);
+      if (l == 0) s.gmass[g] = part;
     }
   }
   __syncthreads();
@@ -1246,7 +1277,31 @@ __device__ __forceinline__ void sample_row16(const KArgs& a, Smem& s, Src& src, 
     }
   }
   __syncthreads();
-  if (wave_id() == 0) resolve16<DT>(s, V, T, kk, p, u, m);
+  if (wave_id() == 0) {
+    // wave 0's slice of a register-resident row goes to LDS while it resolves, so the
+    // searches get the registers the row occupies
+    if constexpr (Src::kStore) {
+      static_assert(sizeof(s.park) >= sizeof(src.r[0]) * 64 * (sizeof(src.r) / sizeof(src.r[0])) ||
+                        (sizeof(src.r) / sizeof(src.r[0])) > PARK_CHUNKS,
+                    "park area");
+      if constexpr ((sizeof(src.r) / sizeof(src.r[0])) <= PARK_CHUNKS) {
+        constexpr int NC = sizeof(src.r) / sizeof(src.r[0]);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) s.park[j * 64 + lane_id()] = src.r[j];
+        // the compiler must not forward the parked values past the search (that would
+        // keep the row live in registers after all)
+        asm volatile("" ::: "memory");
+        resolve16<DT>(s, V, T, kk, p, u, m);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < NC; ++j) src.r[j] = s.park[j * 64 + lane_id()];
+      } else {
+        resolve16<DT>(s, V, T, kk, p, u, m);
+      }
+    } else {
+      resolve16<DT>(s, V, T, kk, p, u, m);
+    }
+  }
   __syncthreads();
   const RowState st = s.st;
   __syncthreads();
