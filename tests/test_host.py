@@ -1,0 +1,169 @@
+"""Host side of the sampler without a GPU: parameter mirror, packing, uniforms, the C ABI's
+exported symbols and argument validation (calls that return before any HIP work).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from pagedbatch_amd import SamplingParams, _lib, sample, sample_token
+from pagedbatch_amd import sampling as smp
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pbsample.h")
+
+
+# ---------------------------------------------------------------- SamplingParams mirror
+@pytest.mark.parametrize("kw,msg", [
+    ({"max_tokens": 0}, "max_tokens must be >= 1"),
+    ({"temperature": -0.1}, "temperature must be >= 0"),
+    ({"top_p": 0.0}, r"top_p must be in \(0, 1\]"),
+    ({"top_p": 1.01}, r"top_p must be in \(0, 1\]"),
+    ({"top_k": -1}, "top_k must be >= 0"),
+])
+def test_sampling_params_validation(kw, msg):
+    """Same errors as pagedbatch/config.py:146-154."""
+    with pytest.raises(ValueError, match=msg):
+        SamplingParams(**kw)
+
+
+def test_sampling_params_defaults():
+    sp = SamplingParams()
+    assert (sp.max_tokens, sp.temperature, sp.top_p, sp.top_k, sp.ignore_eos, sp.seed, sp.stop_token_ids) == \
+        (64, 1.0, 1.0, 0, False, None, ())
+    assert SamplingParams(temperature=0.0).greedy and not sp.greedy
+
+
+# ---------------------------------------------------------------- packing and uniforms
+def test_pack_layout():
+    h = smp._pack(3, [0.0, 0.7, 1.0], [0, 5, 1000], [1.0, 0.9, 0.5], [0.0, 0.25, 0.75], [2, 0, 1], vocab=1000)
+    assert h.dtype == np.int32 and h.shape == (5, 3)
+    assert np.array_equal(h[0].view(np.float32), np.float32([0.0, 0.7, 1.0]))
+    assert list(h[1]) == [0, 5, 0]  # top_k >= vocab is off (sampling.py:15)
+    assert np.array_equal(h[2].view(np.float32), np.float32([1.0, 0.9, 0.5]))
+    assert np.array_equal(h[3].view(np.float32), np.float32([0.0, 0.25, 0.75]))
+    assert list(h[4]) == [2, 0, 1]
+
+
+def test_draw_uniforms_consumes_generators_like_the_reference():
+    """One torch.rand per stochastic row, in row order; greedy rows draw nothing
+    (pagedbatch/sampling.py:12-13 returns before touching the generator)."""
+    shared = torch.Generator().manual_seed(42)
+    params = [SamplingParams(temperature=1.0), SamplingParams(temperature=0.0), SamplingParams(temperature=0.5)]
+    us = smp.draw_uniforms(params, [shared, shared, shared])
+    ref = torch.Generator().manual_seed(42)
+    a, b = float(torch.rand((), generator=ref)), float(torch.rand((), generator=ref))
+    assert us == [a, 0.0, b]
+    # the generator has advanced by exactly two draws
+    assert float(torch.rand((), generator=shared)) == float(torch.rand((), generator=ref))
+
+
+def test_no_cpu_path():
+    x = torch.randn(2, 100)
+    with pytest.raises(ValueError, match="no CPU path"):
+        sample(x, [SamplingParams()] * 2, [torch.Generator()] * 2)
+    with pytest.raises(ValueError):
+        sample_token(torch.randn(3, 4), SamplingParams(), torch.Generator())
+
+
+def test_status_mapping():
+    smp._raise_for_status(np.zeros(4, np.int32))
+    with pytest.raises(RuntimeError, match="probability tensor contains"):
+        smp._raise_for_status(np.array([0, _lib.ROW_NAN], np.int32))
+    with pytest.raises(RuntimeError, match="probability tensor contains"):
+        smp._raise_for_status(np.array([_lib.ROW_NONFINITE], np.int32))
+    with pytest.raises(ValueError):
+        smp._raise_for_status(np.array([0, 0, _lib.ROW_BAD_PARAM], np.int32))
+
+
+# ---------------------------------------------------------------- the C ABI library
+def _header_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(pbs_\w+)\s*\(", text)
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert set(names) == set(_lib.SYMBOLS), (names, _lib.SYMBOLS)
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), n
+    assert lib.pbs_abi_version() == _lib.ABI_VERSION
+    m = re.search(r"#define PBS_ABI_VERSION (\d+)", open(HEADER).read())
+    assert int(m.group(1)) == _lib.ABI_VERSION
+    assert lib.pbs_workspace_bytes(256, 128256, _lib.DTYPE_BF16) == 0
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    consts = dict((k, int(v)) for k, v in re.findall(r"(PBS_\w+)\s*=\s*(-?\d+)", text))
+    assert consts["PBS_DTYPE_F32"] == _lib.DTYPE_F32
+    assert consts["PBS_DTYPE_F16"] == _lib.DTYPE_F16
+    assert consts["PBS_DTYPE_BF16"] == _lib.DTYPE_BF16
+    assert consts["PBS_OK"] == _lib.OK
+    assert consts["PBS_ERR_INVALID_ARGUMENT"] == _lib.ERR_INVALID_ARGUMENT
+    assert consts["PBS_ERR_UNSUPPORTED_DTYPE"] == _lib.ERR_UNSUPPORTED_DTYPE
+    assert consts["PBS_ERR_HIP"] == _lib.ERR_HIP
+    assert consts["PBS_ROW_NAN"] == _lib.ROW_NAN
+    assert consts["PBS_ROW_NONFINITE"] == _lib.ROW_NONFINITE
+    assert consts["PBS_ROW_BAD_PARAM"] == _lib.ROW_BAD_PARAM
+
+
+def test_row_info_layout_matches_c(tmp_path):
+    """offsetof() of every pbs_row_info field, from gcc, against the numpy record type."""
+    fields = _lib.ROW_INFO_DTYPE.names
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "pbsample.h"\nint main(void){\n'
+                   + "".join(f'printf("%zu\\n", offsetof(pbs_row_info, {f}));\n' for f in fields)
+                   + 'printf("%zu\\n", sizeof(pbs_row_info));\nreturn 0;}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    out = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert out[:-1] == [_lib.ROW_INFO_DTYPE.fields[f][1] for f in fields]
+    assert out[-1] == _lib.ROW_INFO_DTYPE.itemsize
+
+
+def _call(lib, **kw):
+    a = dict(logits=1 << 20, dtype=_lib.DTYPE_BF16, n_rows=4, rows=4, vocab=1000, stride=1000, row_map=None,
+             t=1 << 20, k=1 << 20, p=1 << 20, u=1 << 20, tok=1 << 20, st=1 << 20)
+    a.update(kw)
+    return lib.pbs_sample(a["logits"], a["dtype"], a["n_rows"], a["rows"], a["vocab"], a["stride"], a["row_map"],
+                          a["t"], a["k"], a["p"], a["u"], a["tok"], a["st"], None, 0, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    ({"dtype": 7}, _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    ({"rows": -1}, _lib.ERR_INVALID_ARGUMENT, "negative"),
+    ({"vocab": 0}, _lib.ERR_INVALID_ARGUMENT, "vocab"),
+    ({"vocab": (1 << 27) + 1, "stride": (1 << 27) + 1}, _lib.ERR_INVALID_ARGUMENT, "vocab"),
+    ({"stride": 999}, _lib.ERR_INVALID_ARGUMENT, "row_stride"),
+    ({"logits": None}, _lib.ERR_INVALID_ARGUMENT, "null"),
+    ({"u": None}, _lib.ERR_INVALID_ARGUMENT, "null"),
+    ({"n_rows": 2}, _lib.ERR_INVALID_ARGUMENT, "n_logit_rows"),
+])
+def test_abi_rejects_bad_arguments_before_any_device_work(kw, code, msg):
+    """Validation happens on the host before anything is launched (no GPU needed here)."""
+    lib = _lib.load()
+    assert _call(lib, **kw) == code
+    assert msg in _lib.last_error(lib)
+
+
+def test_abi_zero_rows_is_a_no_op():
+    lib = _lib.load()
+    assert _call(lib, rows=0) == _lib.OK
+
+
+def test_debug_outputs_need_info():
+    lib = _lib.load()
+    rc = lib.pbs_sample_debug(1 << 20, _lib.DTYPE_F32, 1, 1, 10, 10, None, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
+                              1 << 20, 1 << 20, 1 << 20, None, None, None, 0, None)
+    assert rc == _lib.ERR_INVALID_ARGUMENT and "out_info" in _lib.last_error(lib)
