@@ -38,11 +38,35 @@ def parse():
                     choices=["mixed256_llama3_bf16", "greedy512_quantized", "nucleus1024_qwen_fp32",
                              "steps8_smollm_mixed"])
     ap.add_argument("--copies", type=int, default=0, help="logits copies to rotate over (default: > 256 MB)")
-    ap.add_argument("--cpu-steps", type=int, default=3, help="CPU baseline steps (median)")
+    ap.add_argument("--cpu-steps", type=int, default=5, help="CPU baseline steps (median)")
     ap.add_argument("--cpu-rows", type=int, default=0, help="CPU baseline rows per step (0: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-parity", action="store_true", help="skip the token check against the oracle")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="time a plain device copy of the workload's logits bytes instead of the sampler "
+                         "(the reference kernel for calibrating HBM byte counters)")
     return ap.parse_args()
+
+
+def copy_only(args, w, torch):
+    """Plain copy of the same byte count as one step's logits (dst <- src, rotating buffers)."""
+    nbytes = w.rows * w.vocab * w.logits.element_size()
+    copies = args.copies or max(2, -(-300_000_000 // nbytes))
+    src = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(copies)]
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    for i in range(args.warmup):
+        dst.copy_(src[i % copies])
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for i in range(args.steps):
+        dst.copy_(src[i % copies])
+    g1.record()
+    torch.cuda.synchronize()
+    ms = g0.elapsed_time(g1) / args.steps
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "steps": args.steps,
+                      "ms_per_copy": round(ms, 5), "GBps_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}),
+          flush=True)
 
 
 def cpu_baseline(w, steps: int, rows: int):
@@ -91,6 +115,9 @@ def main():
     lib = _lib.load()
     print(f"[bench] building workload {args.workload}", file=sys.stderr, flush=True)
     w = workloads.WORKLOADS[args.workload]()
+    if args.copy_only:
+        copy_only(args, w, torch)
+        return
     rows, vocab = w.rows, w.vocab
     elt = w.logits.element_size()
     alg_bytes = rows * vocab * elt

@@ -32,11 +32,11 @@
 
 namespace pbs {
 
-constexpr int NT = 1024;           // threads per workgroup: one workgroup per row
+constexpr int NT = 512;            // threads per workgroup: one workgroup per row
 constexpr int NWAVE = NT / 64;     // wave64
 constexpr int HIST_WORDS = 32768;  // 64K packed u16 counters = 128 KB of LDS
 constexpr int NGROUP = 256;        // histogram groups of 256 ords (high byte of a 16-bit ord)
-constexpr int PARK_CHUNKS = 16;    // register-row chunks wave 0 can park in LDS
+constexpr int PIPE = 16;           // 16-byte loads per thread in flight while a row streams in
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -355,17 +355,15 @@ struct RowState {
 };
 
 struct __align__(16) Smem {
-  uint32_t hist[HIST_WORDS];     // 16-bit rows: packed u16 counts per ord; reused by index selection
+  uint32_t hist[HIST_WORDS];     // 16-bit rows: packed u16 count per raw pattern; reused by index selection
   uint32_t gcount[NGROUP];       // count of each group of 256 ords
   uint32_t gabove_cnt[NGROUP];   // count strictly above the group (descending order)
   double gmass[NGROUP];          // fp64 mass of each group
   double gabove_mass[NGROUP];    // mass strictly above the group
-  u4 park[PARK_CHUNKS * 64];     // wave 0's register row slice while it runs resolve16
-  uint32_t gc_n[256];            // bins of the group a 16-bit search is in: counts
-  double gc_w[256];              // and masses, by bin offset inside the group
   double red_d[NWAVE];
   float red_f[NWAVE];
   int red_i[2 * NWAVE];
+  uint32_t nan_cnt;              // 16-bit rows: elements in the NaN / inf raw blocks
   int sel_jstar, sel_rank, sel_index;
   RowState st;
 };
@@ -468,6 +466,7 @@ struct RegRow {
   static constexpr int EPV = DTraits<DT>::EPV;
   static constexpr bool kStore = true;
   static constexpr bool kVector = true;
+  static constexpr int D = NCH < PIPE ? NCH : PIPE;  // loads in flight per thread
   u4 r[NCH];
   const u4* row;
   int nvec;
@@ -480,15 +479,30 @@ struct RegRow {
   // Raw buffer loads: one VGPR offset (the thread's) for every chunk, the chunk offset in
   // an SGPR, and the buffer's range check returning zeros past the row end, so the code
   // stays straight-line and the compiler waits for each chunk only when it is first used.
-  // Non-temporal: the row is read exactly once.
-  __device__ __forceinline__ void load() {
+  // Non-temporal: the row is read from memory exactly once.
+  __device__ __forceinline__ void load_chunk(int j) {
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, nvec * 16, 0x00020000);
-#pragma unroll
-    for (int j = 0; j < NCH; ++j)
-      r[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, j * NT * 16, 2));
+    r[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, j * NT * 16, 2));
   }
-  // f(j, q, base_index, valid): q is the 16-byte vector, base_index its first element
+  // issues the first D chunks; stream() issues the rest as it consumes the row
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int j = 0; j < D; ++j) load_chunk(j);
+  }
+  // The first pass: f(j, q, base_index, valid) on chunk j while chunk j + D loads, so the
+  // work on the row overlaps its arrival. Every chunk stays in registers for later passes.
+  template <class F>
+  __device__ __forceinline__ void stream(F&& f) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j + D < NCH) load_chunk(j + D);
+      const int v = j * NT + (int)threadIdx.x;
+      f(j, r[j], v * EPV, v < nvec);
+      __builtin_amdgcn_sched_barrier(0);  // keeps the loads interleaved with the work
+    }
+  }
+  // later passes over the resident row
   template <class F>
   __device__ __forceinline__ void for_each(F&& f) const {
 #pragma unroll
@@ -498,7 +512,6 @@ struct RegRow {
     }
   }
   __device__ __forceinline__ int nchunks() const { return NCH; }
-  __device__ __forceinline__ void store(int j, const u4& q) { r[j] = q; }
 };
 
 template <int DT>
@@ -524,8 +537,11 @@ struct MemRow {
       f(j, q, v * EPV, v < nvec);
     }
   }
+  template <class F>
+  __device__ __forceinline__ void stream(F&& f) const {
+    for_each(f);
+  }
   __device__ __forceinline__ int nchunks() const { return (nvec + NT - 1) / NT; }
-  __device__ __forceinline__ void store(int, const u4&) {}
 };
 
 template <int DT>
@@ -563,8 +579,11 @@ struct ScalarRow {
       f(j, q, v * EPV, v < nvec);
     }
   }
+  template <class F>
+  __device__ __forceinline__ void stream(F&& f) const {
+    for_each(f);
+  }
   __device__ __forceinline__ int nchunks() const { return (nvec + NT - 1) / NT; }
-  __device__ __forceinline__ void store(int, const u4&) {}
 };
 
 template <class Src>
@@ -653,28 +672,33 @@ __device__ __forceinline__ int select_index(const Src& src, Smem& s, M&& match, 
 }
 
 // Index selection for register-resident 16-bit rows: the rank-th lowest-index element
-// whose (unfolded) ord lies in [lo, lo + span]. Per-(chunk, wave) match counts come from
+// whose key lies in [lo, lo + span]. The key is the raw 16-bit pattern (ORD = false: a
+// range of values of one sign is a contiguous range of raws) or the unfolded ord (ORD =
+// true: ranges that take in both -0 and +0). Per-(chunk, wave) match counts come from
 // ballots of the per-element compares (scalar popcounts, skipped where the wave has no
-// match in the chunk), so the pass costs about two VALU ops per element; only the wave
-// holding the answer then looks at its lanes.
+// match in the chunk); only the wave holding the answer then looks at its lanes.
 __device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
 }
-template <int DT, int NCH>
-__device__ __forceinline__ uint32_t match_bits16(const RegRow<DT, NCH>& src, int j, uint32_t lo2, uint32_t span) {
+template <bool ORD>
+__device__ __forceinline__ uint32_t key16x2(uint32_t w) {
+  if constexpr (ORD) return ord16_pair(w);
+  else return w;
+}
+// match bits of the 8 elements of one 16-byte vector (bit e for element e)
+template <bool ORD>
+__device__ __forceinline__ uint32_t match_bits16(const u4& q, uint32_t lo2, uint32_t span) {
   uint32_t bits = 0;
-  if (j * NT + (int)threadIdx.x < src.nvec) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t dl = pk_sub_u16(ord16_pair(src.r[j][d]), lo2);
-      bits |= ((dl & 0xffffu) <= span ? 1u : 0u) << (2 * d);
-      bits |= ((dl >> 16) <= span ? 1u : 0u) << (2 * d + 1);
-    }
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t dl = pk_sub_u16(key16x2<ORD>(q[d]), lo2);
+    bits |= ((dl & 0xffffu) <= span ? 1u : 0u) << (2 * d);
+    bits |= ((dl >> 16) <= span ? 1u : 0u) << (2 * d + 1);
   }
   return bits;
 }
 
-template <int DT, int NCH>
+template <bool ORD, int DT, int NCH>
 __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Smem& s, uint32_t lo, uint32_t span,
                                                   int rank) {
   static_assert(NCH * NWAVE <= 256, "chunk table must fit 4 entries per lane");
@@ -687,7 +711,7 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
     uint64_t any = 0;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t dl = pk_sub_u16(ord16_pair(src.r[j][d]), lo2);
+      const uint32_t dl = pk_sub_u16(key16x2<ORD>(src.r[j][d]), lo2);
       mk[2 * d] = ballot(vv && (dl & 0xffffu) <= span);
       mk[2 * d + 1] = ballot(vv && (dl >> 16) <= span);
       any |= mk[2 * d] | mk[2 * d + 1];
@@ -738,10 +762,12 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
   if (pos >= 0) {
     const int jstar = pos / NWAVE, wstar = pos % NWAVE, rr = s.sel_rank;
     if (w == wstar) {
-      uint32_t bits = 0;
+      // chunk jstar by a select chain on the (wave-uniform) index: one vector live, not NCH
+      u4 q = src.r[0];
 #pragma unroll
-      for (int j = 0; j < NCH; ++j)
-        if (j == jstar) bits = match_bits16(src, j, lo2, span);
+      for (int j = 1; j < NCH; ++j)
+        if (j == jstar) q = src.r[j];
+      const uint32_t bits = (jstar * NT + (int)threadIdx.x < src.nvec) ? match_bits16<ORD>(q, lo2, span) : 0u;
       const uint32_t cnt = (uint32_t)__popc(bits);
       const uint32_t incl = wscan_u32(cnt);
       const uint32_t excl = incl - cnt;
@@ -786,443 +812,469 @@ __device__ __forceinline__ void write_error(const KArgs& a, int b, int status, f
 }
 
 // ---------------------------------------------------------------------------------------
-// 16-bit rows: searches over the LDS histogram
+// 16-bit rows: the histogram
+//
+// hist counts every raw 16-bit pattern r of the row in half (r & 1) of word r >> 1 (u16
+// counters). Ords map to raws one to one (raw_of_ord16), and the 256 ords of a group g
+// are one aligned block of 256 raws: block g - 128 for g >= 128 (non-negative values, raw
+// ascending with the ord) and block 255 - g below (negative values, raw descending).
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t hist_count(const Smem& s, uint32_t o) {
-  const uint32_t w = s.hist[o >> 1];
-  return (o & 1u) ? (w >> 16) : (w & 0xffffu);
+// unfolded ord of one raw: -0 gets 0x7fff, +0 0x8000 (adjacent, and tied after scaling)
+__device__ __forceinline__ uint32_t ord16u(uint32_t raw) { return raw ^ ((raw & 0x8000u) ? 0xffffu : 0x8000u); }
+
+__device__ __forceinline__ uint32_t hist_count_raw(const Smem& s, uint32_t raw) {
+  const uint32_t w = s.hist[raw >> 1];
+  return (raw & 1u) ? (w >> 16) : (w & 0xffffu);
+}
+__device__ __forceinline__ uint32_t hist_count(const Smem& s, uint32_t o) { return hist_count_raw(s, raw_of_ord16(o)); }
+
+// counts of ords o0 .. o0+3 (o0 % 4 == 0), in ord order: one 8-byte LDS read
+__device__ __forceinline__ void counts4(const Smem& s, uint32_t o0, uint32_t n[4]) {
+  if (o0 & 0x8000u) {
+    const uint32_t* h = &s.hist[(o0 & 0x7fffu) >> 1];
+    const uint32_t w0 = h[0], w1 = h[1];
+    n[0] = w0 & 0xffffu;
+    n[1] = w0 >> 16;
+    n[2] = w1 & 0xffffu;
+    n[3] = w1 >> 16;
+  } else {
+    // raws 0xfffc - o0 .. 0xffff - o0 hold ords o0 + 3 .. o0
+    const uint32_t* h = &s.hist[(0xfffcu - o0) >> 1];
+    const uint32_t w0 = h[0], w1 = h[1];
+    n[3] = w0 & 0xffffu;
+    n[2] = w0 >> 16;
+    n[1] = w1 & 0xffffu;
+    n[0] = w1 >> 16;
+  }
+}
+
+// Adds the two 16-bit values packed in w. The byte address of raw r's counter word is
+// (r >> 1) * 4, and the increment 1 << 16 * (r & 1); the packed 16-bit shift puts each
+// value's low bit at bit 4 of its own half, where the 32-bit shift reads its amount.
+__device__ __forceinline__ void hist_add_pair(Smem& s, uint32_t w) {
+  const uint32_t t = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, w) << (u16x2){4, 4});
+  uint8_t* h = (uint8_t*)s.hist;
+  __hip_atomic_fetch_add((uint32_t*)(h + ((w << 1) & 0x1fffcu)), 1u << (t & 31u), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+  __hip_atomic_fetch_add((uint32_t*)(h + ((w >> 15) & 0x1fffcu)), 1u << ((t >> 16) & 31u), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void hist_add_one(Smem& s, uint32_t raw) {
+  __hip_atomic_fetch_add(&s.hist[raw >> 1], 1u << ((raw & 1u) << 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 template <int DT>
-__device__ __forceinline__ float scaled16(uint32_t o, float T) {
-  return raw_to_float<DT>(raw_of_ord16(o)) / T;
+__device__ __forceinline__ float scaled16(uint32_t o, const Divider& dv) {
+  return dv(raw_to_float<DT>(raw_of_ord16(o)));
 }
-// softmax weight of one distinct 16-bit value relative to the row maximum m, in fp64 from
-// the exact fp32 scaled value (pagedbatch takes softmax of the fp32 scaled row, sampling.py:26)
+// softmax weight of one distinct value relative to the row maximum m, in fp64 from the
+// exact fp32 scaled value (pagedbatch takes softmax of the fp32 scaled row, sampling.py:26)
 template <int DT>
-__device__ __forceinline__ double weight16(uint32_t o, float T, float m) {
-  return weight_f(scaled16<DT>(o, T), m);
-}
-
-// The bins of one group, cached in LDS by wave 0 for the searches of resolve16: counts
-// and masses by bin offset. Lane l works on the bins at descending positions 4l..4l+3,
-// i.e. offsets 255-4l-i.
-template <int DT>
-__device__ __forceinline__ void load_group(Smem& s, uint32_t g, float T, float m) {
-  const int l = lane_id();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t off = (uint32_t)(4 * l + i);
-    const uint32_t n = hist_count(s, g * 256u + off);
-    s.gc_n[off] = n;
-    s.gc_w[off] = n ? (double)n * weight16<DT>(g * 256u + off, T, m) : 0.0;
-  }
-}
-
-// count and mass of the cached group's bins with ord >= t
-__device__ __forceinline__ void group_ge(const Smem& s, uint32_t g, uint32_t t, uint32_t& cnt, double& mass) {
-  const int l = lane_id();
-  uint32_t c = 0;
-  double ms = 0.0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t off = (uint32_t)(4 * l + i);
-    if (g * 256u + off >= t) {
-      c += s.gc_n[off];
-      ms += s.gc_w[off];
-    }
-  }
-  cnt = wsum_u32(c);
-  mass = wsum_f64(ms);
-}
-
-// first ord >= lo of the cached group (descending) whose inclusive count from the top of
-// the group reaches need
-__device__ __forceinline__ uint32_t group_find_count(const Smem& s, uint32_t g, uint32_t lo, uint32_t need) {
-  const int l = lane_id();
-  uint32_t n[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t off = 255u - (uint32_t)(4 * l + i);
-    n[i] = (g * 256u + off >= lo) ? s.gc_n[off] : 0u;
-  }
-  const uint32_t tot = n[0] + n[1] + n[2] + n[3];
-  const uint32_t incl = wscan_u32(tot);
-  const uint64_t hit = ballot(incl >= need);
-  const int L = hit ? first_lane(hit) : 63;
-  uint32_t run = incl - tot;
-  int found = 3;
-  bool done = false;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (!done && run + n[i] >= need) {
-      found = i;
-      done = true;
-    }
-    run += n[i];
-  }
-  return g * 256u + 255u - bcast_u32((uint32_t)(4 * l + found), L);
-}
-
-// first ord >= lo of the cached group (descending) whose inclusive mass, starting from
-// `base` above the group, exceeds target; the lowest non-empty ord >= lo if rounding keeps
-// the cumulative at or below the target
-__device__ __forceinline__ uint32_t group_find_mass(const Smem& s, uint32_t g, uint32_t lo, double base,
-                                                    double target) {
-  const int l = lane_id();
-  double w[4];
-  uint32_t any = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t off = 255u - (uint32_t)(4 * l + i);
-    const bool in = g * 256u + off >= lo;
-    w[i] = in ? s.gc_w[off] : 0.0;
-    any |= (in && s.gc_n[off]) ? (1u << i) : 0u;
-  }
-  const double tot = w[0] + w[1] + w[2] + w[3];
-  const double incl = wscan_f64(tot);
-  double excl = __shfl_up(incl, 1);
-  if (l == 0) excl = 0.0;
-  uint64_t hit = ballot(base + incl > target);
-  bool last = false;
-  if (!hit) {
-    hit = ballot(any != 0u);
-    last = true;
-  }
-  const int L = last ? 63 - __clzll((unsigned long long)hit) : first_lane(hit);
-  double run = base + excl;
-  int found = -1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool take = last ? ((any >> i) & 1u) != 0u : (found < 0 && run + w[i] > target);
-    if (take) found = i;
-    run += w[i];
-  }
-  return g * 256u + 255u - bcast_u32((uint32_t)(4 * l + (found < 0 ? 3 : found)), L);
+__device__ __forceinline__ double weight16(uint32_t o, const Divider& dv, float m) {
+  return weight_f(scaled16<DT>(o, dv), m);
 }
 
 // Ords whose scaled value equals that of ord o. Distinct 16-bit values only meet after the
-// division by T at the under/overflow ends; the map is monotone, so binary search.
+// division by T at the under/overflow ends (and -0 meets +0); the map is monotone, so
+// binary search.
 template <int DT>
-__device__ __forceinline__ void tie_range16(uint32_t o, float T, uint32_t& lo, uint32_t& hi) {
-  const float x = scaled16<DT>(o, T);
+__device__ __forceinline__ void tie_range16(uint32_t o, const Divider& dv, uint32_t& lo, uint32_t& hi) {
+  const float x = scaled16<DT>(o, dv);
   uint32_t a = ord16_neg_inf<DT>(), b = o;
-  if (o == 0u || scaled16<DT>(o - 1u, T) < x) {
+  if (o <= a || scaled16<DT>(o - 1u, dv) < x) {
     a = o;
   } else {
     while (a < b) {
       const uint32_t mid = a + (b - a) / 2;
-      if (scaled16<DT>(mid, T) >= x) b = mid; else a = mid + 1;
+      if (scaled16<DT>(mid, dv) >= x) b = mid; else a = mid + 1;
     }
   }
   lo = a;
   a = o;
   b = ord16_pos_inf<DT>();
-  if (o >= b || scaled16<DT>(o + 1u, T) > x) {
+  if (o >= b || scaled16<DT>(o + 1u, dv) > x) {
     b = o;
   } else {
     while (a < b) {
       const uint32_t mid = a + (b - a + 1) / 2;
-      if (scaled16<DT>(mid, T) <= x) a = mid; else b = mid - 1;
+      if (scaled16<DT>(mid, dv) <= x) a = mid; else b = mid - 1;
     }
   }
   hi = a;
 }
 
-// The group holding the need-th element (descending) of ords >= lo, whose partial lowest
-// group holds cnt_lo; -1 if fewer elements.
-__device__ __forceinline__ int find_group_count(const Smem& s, uint32_t lo, uint32_t cnt_lo, uint32_t need) {
+// ---------------------------------------------------------------------------------------
+// searches over one group, run by one wave. Lane l holds the four ords
+// g*256 + 255 - 4l - i (i = 0..3), i.e. the group in descending order.
+// ---------------------------------------------------------------------------------------
+struct GroupHit {
+  uint32_t o;         // the ord found
+  uint32_t cnt_excl;  // elements of the group above o (ords in range only)
+  double mass_excl;   // their mass
+  uint32_t cnt;       // elements at o
+};
+
+// BY_MASS: the first ord >= lo (descending) whose inclusive mass from the group top exceeds
+// `target`; if rounding keeps every cumulative at or below it, the lowest non-empty ord >= lo.
+// Otherwise: the first ord >= lo whose inclusive count reaches `need`. Either way the
+// count and mass of the group's elements above the ord come with it.
+template <int DT, bool BY_MASS>
+__device__ __forceinline__ GroupHit group_search(const Smem& s, uint32_t g, uint32_t lo, const Divider& dv, float m,
+                                                 uint32_t need, double target) {
+  const int l = lane_id();
+  uint32_t n4[4];
+  counts4(s, g * 256u + 252u - 4u * (uint32_t)l, n4);
+  uint32_t c[4];
+  double w[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t o = g * 256u + 255u - 4u * (uint32_t)l - (uint32_t)i;
+    c[i] = (o >= lo) ? n4[3 - i] : 0u;
+    if (c[i]) w[i] = (double)c[i] * weight16<DT>(o, dv, m);
+  }
+  const uint32_t ct = c[0] + c[1] + c[2] + c[3];
+  const uint32_t ci = wscan_u32(ct);
+  const double wt = ((w[0] + w[1]) + w[2]) + w[3];
+  const double wi = wscan_f64(wt);
+  uint64_t hit = BY_MASS ? ballot(wi > target) : ballot(ci >= need);
+  bool last = false;
+  if (!hit) {
+    hit = ballot(ct != 0u);
+    last = true;
+  }
+  // (an empty range cannot reach here from the searches below; lane 0 keeps it in bounds)
+  const int L = !hit ? 0 : last ? 63 - __clzll((unsigned long long)hit) : first_lane(hit);
+  uint32_t rc = ci - ct;
+  double rw = wi - wt;
+  int found = -1;
+  uint32_t fc = 0u;
+  double fw = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bool take;
+    if (last) take = c[i] != 0u;  // keeps the lowest non-empty one
+    else if (BY_MASS) take = found < 0 && rw + w[i] > target;
+    else take = found < 0 && rc + c[i] >= need;
+    if (take) {
+      found = i;
+      fc = rc;
+      fw = rw;
+    }
+    rc += c[i];
+    rw += w[i];
+  }
+  if (found < 0) found = 3;
+  GroupHit h;
+  h.o = g * 256u + 255u - bcast_u32(4u * (uint32_t)l + (uint32_t)found, L);
+  h.cnt_excl = bcast_u32(fc, L);
+  h.mass_excl = bcast_f64(fw, L);
+  h.cnt = bcast_u32(c[found], L);
+  return h;
+}
+
+// count and mass of the elements with ord >= t (whole wave)
+template <int DT>
+__device__ __forceinline__ void count_mass_ge(const Smem& s, uint32_t t, const Divider& dv, float m, uint32_t& cnt,
+                                              double& mass) {
+  if (t > 0xffffu) {
+    cnt = 0u;
+    mass = 0.0;
+    return;
+  }
+  const uint32_t g = t >> 8;
+  const int l = lane_id();
+  uint32_t n4[4];
+  counts4(s, g * 256u + 4u * (uint32_t)l, n4);
+  uint32_t c = 0u;
+  double w = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t o = g * 256u + 4u * (uint32_t)l + (uint32_t)i;
+    if (o >= t && n4[i]) {
+      c += n4[i];
+      w += (double)n4[i] * weight16<DT>(o, dv, m);
+    }
+  }
+  cnt = wsum_u32(c) + s.gabove_cnt[g];
+  mass = wsum_f64(w) + s.gabove_mass[g];
+}
+
+// the group holding the need-th element (descending) among ords >= lo; -1 if none
+__device__ __forceinline__ int find_group_count(const Smem& s, uint32_t lo, uint32_t need) {
   const int l = lane_id();
   const uint32_t glo = lo >> 8;
   int found = -1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t g = (uint32_t)(4 * l + i);
+    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
     const uint32_t ab = s.gabove_cnt[g];
-    const uint32_t c = g > glo ? s.gcount[g] : (g == glo ? cnt_lo : 0u);
-    if (c && ab < need && need <= ab + c) found = (int)g;
+    if (g >= glo && s.gcount[g] && ab < need && need <= ab + s.gcount[g]) found = (int)g;
   }
   const uint64_t hit = ballot(found >= 0);
   return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
 }
 
-// The group whose cumulative mass interval [above, above + mass) holds target, over ords
-// >= lo whose partial lowest group holds mass_lo. Groups tile the cumulative exactly
-// because each group's upper end is the next lower group's stored "above".
-__device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, double mass_lo, double total,
-                                                         double target) {
+// the group whose cumulative mass interval [above, above + mass) holds target, among
+// groups >= lo >> 8 (the caller makes sure target lies above the range's lower end)
+__device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, double target) {
   const int l = lane_id();
   const uint32_t glo = lo >> 8;
   int found = -1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t g = (uint32_t)(4 * l + i);
-    if (g < glo) continue;
+    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
     const double ab = s.gabove_mass[g];
-    const double end = (g == glo) ? ab + mass_lo : (g == 0 ? total : s.gabove_mass[g - 1]);
-    const bool nonempty = (g == glo) ? mass_lo > 0.0 : s.gmass[g] > 0.0;
-    if (nonempty && ab <= target && target < end) found = (int)g;
+    if (g >= glo && s.gmass[g] > 0.0 && ab <= target && target < ab + s.gmass[g]) found = (int)g;
   }
   const uint64_t hit = ballot(found >= 0);
   return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
 }
 
-// Index of the rank-th lowest-index element whose ord lies in [lo, hi] (-0 counts as +0).
+// A tie group located by a search: its ord range, count, mass above it and per-element
+// weight.
+struct TieGroup {
+  uint32_t lo, hi;
+  uint32_t n;        // elements with ord in [lo, hi]
+  uint32_t n_above;  // elements above hi
+  double above;      // mass above hi
+  double w;          // weight of one element
+};
+
+template <int DT>
+__device__ __forceinline__ TieGroup tie_group(const Smem& s, uint32_t g, const GroupHit& h, uint32_t range_lo,
+                                              const Divider& dv, float m) {
+  TieGroup t;
+  tie_range16<DT>(h.o, dv, t.lo, t.hi);
+  t.lo = max(t.lo, range_lo);
+  t.w = weight16<DT>(h.o, dv, m);
+  if (t.lo == h.o && t.hi == h.o) {
+    t.n = h.cnt;
+    t.n_above = s.gabove_cnt[g] + h.cnt_excl;
+    // mass above from the group prefix plus the group's own scan
+    t.above = s.gabove_mass[g] + h.mass_excl;
+  } else {
+    uint32_t c_ge;
+    double m_ge;
+    count_mass_ge<DT>(s, t.hi + 1u, dv, m, t.n_above, t.above);
+    count_mass_ge<DT>(s, t.lo, dv, m, c_ge, m_ge);
+    t.n = c_ge - t.n_above;
+  }
+  return t;
+}
+
+// Top-k threshold, top-p cutoff and draw position from the histogram summaries. Runs on
+// wave 0 only and leaves the result in s.st (written by lane 0). Returns false if a u16
+// counter wrapped (one value more than 65535 times): the caller then takes the general path.
+template <int DT>
+__device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int kk, float p, float u, float m) {
+  const int l = lane_id();
+  const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
+  if (total_cnt != (uint32_t)V) return false;
+  RowState st = {};
+  st.status = PBS_ROW_OK;
+  st.m = m;
+  st.x_kth = -INFINITY;
+  const double z_all = s.gabove_mass[0] + s.gmass[0];
+
+  // top-k (sampling.py:15-17): K = ords >= the tie group of the k-th largest element
+  uint32_t k_lo = 0u;
+  uint32_t nk = (uint32_t)V;
+  double zk = z_all;
+  TieGroup kt = {};
+  const bool topk = kk > 0 && kk < V;
+  if (topk) {
+    const int g = find_group_count(s, 0u, (uint32_t)kk);
+    if (g < 0) return false;
+    const GroupHit h = group_search<DT, false>(s, (uint32_t)g, 0u, dv, m, (uint32_t)kk - s.gabove_cnt[g], 0.0);
+    kt = tie_group<DT>(s, (uint32_t)g, h, 0u, dv, m);
+    k_lo = kt.lo;
+    st.x_kth = scaled16<DT>(h.o, dv);
+    uint32_t c_ge;
+    count_mass_ge<DT>(s, k_lo, dv, m, c_ge, zk);
+    nk = c_ge;
+  }
+  st.zk = zk;
+
+  // top-p (sampling.py:18-25): keep the shortest prefix whose exclusive mass is <= p * Z_K
+  TieGroup ct;
+  int n_keep;
+  double zp;
+  const double tau = (double)p * zk;
+  int gc = -1;
+  GroupHit hc = {};
+  if (p < 1.0f) {
+    gc = find_group_mass(s, k_lo, tau);
+    if (gc >= 0) hc = group_search<DT, true>(s, (uint32_t)gc, k_lo, dv, m, 0u, tau - s.gabove_mass[gc]);
+  }
+  if (gc >= 0) {
+    ct = tie_group<DT>(s, (uint32_t)gc, hc, k_lo, dv, m);
+    const double kf = (ct.w > 0.0) ? floor((tau - ct.above) / ct.w) + 1.0 : (double)ct.n;
+    n_keep = (int)fmax(1.0, fmin(kf, (double)ct.n));
+    zp = ct.above + (double)n_keep * ct.w;
+    st.n_kept = (int)ct.n_above + n_keep;
+  } else {
+    // all of K is kept; the cutoff group is K's lowest value
+    if (topk) {
+      ct = kt;
+    } else {
+      const int g = find_group_count(s, 0u, nk);
+      if (g < 0) return false;
+      const GroupHit h = group_search<DT, false>(s, (uint32_t)g, 0u, dv, m, nk - s.gabove_cnt[g], 0.0);
+      ct = tie_group<DT>(s, (uint32_t)g, h, 0u, dv, m);
+    }
+    n_keep = (int)ct.n;
+    zp = zk;
+    st.n_kept = (int)nk;
+  }
+  st.x_cut = scaled16<DT>(ct.hi, dv);
+  st.n_cut_tie = (int)ct.n;
+  st.n_cut_keep = n_keep;
+  st.zp = zp;
+  st.cut_lo = ct.lo;
+  st.cut_hi = ct.hi;
+  st.kord_lo = k_lo;
+
+  // draw (sampling.py:26-27, inverse-CDF form): the first kept element whose cumulative
+  // mass exceeds u * Z_P; it lies in the cutoff group unless t < the mass above it
+  const double t = (double)u * zp;
+  st.target = t;
+  TieGroup dt = ct;
+  int n_avail = n_keep;
+  if (t < ct.above) {
+    int g = find_group_mass(s, ct.hi + 1u, t);
+    if (g < 0) g = (int)(ct.hi >> 8);  // rounding at a group edge: search the cutoff's own group
+    const GroupHit h = group_search<DT, true>(s, (uint32_t)g, ct.hi + 1u, dv, m, 0u, t - s.gabove_mass[g]);
+    dt = tie_group<DT>(s, (uint32_t)g, h, ct.hi + 1u, dv, m);
+    n_avail = (int)dt.n;
+  }
+  st.sel_lo = dt.lo;
+  st.sel_hi = dt.hi;
+  st.sel_n = n_avail;
+  st.sel_rank = (int)fmax(0.0, fmin((dt.w > 0.0) ? floor((t - dt.above) / dt.w) : 0.0, (double)(n_avail - 1)));
+  if (l == 0) s.st = st;
+  return true;
+}
+
+// Index of the rank-th lowest-index element whose ord lies in [lo, hi].
 template <int DT, class Src>
 __device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank) {
-  // -0 carries ord 0x7fff in the unfolded pair encoding and belongs with +0 (0x8000)
-  const uint32_t lo_u = (lo == 0x8000u) ? 0x7fffu : lo;
-  const uint32_t span = hi - lo_u;
   if constexpr (Src::kStore) {
-    return select_index_reg16(src, s, lo_u, span, rank);
+    // values of one sign: a contiguous range of raws (non-negative ords lo.. map to raws
+    // lo - 0x8000.., negative ones to raws 0xffff - hi ..)
+    if (lo >= 0x8000u || hi < 0x8000u)
+      return select_index_reg16<false>(src, s, lo >= 0x8000u ? lo - 0x8000u : 0xffffu - hi, hi - lo, rank);
+    // a range taking in both -0 and +0 (rare): the general selection on ords
+    return select_index<DT>(src, s, [=](uint32_t raw) { return ord16u(raw) - lo <= hi - lo; }, rank);
   } else {
-    return select_index<DT>(src, s, [=](uint32_t raw) { return (ord16_pair(raw) & 0xffffu) - lo_u <= span; }, rank);
+    return select_index<DT>(src, s, [=](uint32_t raw) { return ord16u(raw) - lo <= hi - lo; }, rank);
   }
 }
 
 // ---------------------------------------------------------------------------------------
 // 16-bit stochastic row
 // ---------------------------------------------------------------------------------------
-
-// Top-k threshold, top-p cutoff and draw position from the histogram summaries. Runs on
-// wave 0 only and leaves the result in s.st. The three searches share one loop body (one
-// copy of the code in the instruction cache); the bins of the group being searched are
-// cached in LDS, which keeps the loop's register footprint small.
-template <int DT>
-__device__ __forceinline__ void resolve16(Smem& s, int V, float T, int kk, float p, float u, float m) {
-  const int l = lane_id();
-  RowState& st = s.st;  // written by lane 0
-  if (l == 0) {
-    st = RowState{};
-    st.status = PBS_ROW_OK;
-    st.m = m;
-    st.x_kth = -INFINITY;
-  }
-  const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
-  const double total_mass = s.gabove_mass[0] + s.gmass[0];
-  // a u16 counter wraps only if one value occurs more than 65535 times
-  if (total_cnt != (uint32_t)V) {
-    if (l == 0) st.status = -1;
-    return;
-  }
-  uint32_t cached = 0xffffffffu;
-  uint32_t kord_lo = 0u, nk = (uint32_t)V, cut_hi = 0u;
-  double zk = total_mass, B_cut = 0.0, t = 0.0;
-#pragma unroll 1
-  for (int q = 0; q < 3; ++q) {
-    // q = 0: k-th largest (count k over all ords); q = 1: top-p cutoff (mass p*Z over K) or
-    // the lowest value of K (count |K|); q = 2: draw point (mass u*Z_P above the cutoff group)
-    bool by_mass = false;
-    uint32_t lo = 0u, need = 0u;
-    double target = 0.0;
-    if (q == 0) {
-      if (!(kk > 0 && kk < V)) continue;
-      need = (uint32_t)kk;
-    } else if (q == 1) {
-      lo = kord_lo;
-      by_mass = p < 1.0f;
-      target = (double)p * zk;
-      need = nk;
-    } else {
-      if (!(t < B_cut)) break;
-      lo = cut_hi + 1u;
-      by_mass = true;
-      target = t;
-    }
-    // the partial lowest group of the range, then the group the search lands in
-    const uint32_t glo = lo >> 8;
-    if (cached != glo) {
-      load_group<DT>(s, glo, T, m);
-      cached = glo;
-    }
-    uint32_t cnt_lo;
-    double mass_lo;
-    group_ge(s, glo, lo, cnt_lo, mass_lo);
-    int g = -1;
-    if (by_mass) g = find_group_mass(s, lo, mass_lo, total_mass, target);
-    if (g < 0 && (q == 1 || !by_mass)) {
-      by_mass = false;  // q = 1 with p*Z reaching all of K: the cutoff group is K's lowest value
-      g = find_group_count(s, lo, cnt_lo, need);
-    }
-    if (g < 0) break;
-    if (cached != (uint32_t)g) {
-      load_group<DT>(s, (uint32_t)g, T, m);
-      cached = (uint32_t)g;
-    }
-    const uint32_t o = by_mass ? group_find_mass(s, (uint32_t)g, lo, s.gabove_mass[g], target)
-                               : group_find_count(s, (uint32_t)g, lo, need - s.gabove_cnt[g]);
-    uint32_t tlo, thi;
-    tie_range16<DT>(o, T, tlo, thi);
-    tlo = max(tlo, lo);
-    // count and mass above each end of the tie group
-    uint32_t n_above = 0u, n_ge = 0u;
-    double B = 0.0, mass_ge_lo = 0.0;
-#pragma unroll 1
-    for (int k = 0; k < 2; ++k) {
-      const uint32_t tt = (k == 0) ? thi + 1u : tlo;
-      uint32_t c = 0u;
-      double ms = 0.0;
-      if (tt <= 0xffffu) {
-        const uint32_t gg = tt >> 8;
-        if (cached != gg) {
-          load_group<DT>(s, gg, T, m);
-          cached = gg;
-        }
-        group_ge(s, gg, tt, c, ms);
-        c += s.gabove_cnt[gg];
-        ms += s.gabove_mass[gg];
-      }
-      if (k == 0) {
-        n_above = c;
-        B = ms;
-      } else {
-        n_ge = c;
-        mass_ge_lo = ms;
-      }
-    }
-    const int n_tie = (int)(n_ge - n_above);
-    const double w = weight16<DT>(o, T, m);
-    if (q == 0) {
-      kord_lo = tlo;
-      nk = n_ge;
-      zk = mass_ge_lo;
-      if (l == 0) st.x_kth = scaled16<DT>(o, T);
-    } else if (q == 1) {
-      int n_keep = n_tie;
-      double zp = zk;
-      if (by_mass) {
-        double kf = (w > 0.0) ? floor((target - B) / w) + 1.0 : (double)n_tie;
-        n_keep = (int)fmax(1.0, fmin(kf, (double)n_tie));
-        zp = B + (double)n_keep * w;
-      }
-      // draw (sampling.py:26-27, inverse-CDF form): the first kept element whose
-      // cumulative mass exceeds u * Z_P; it lies in the cutoff group unless t < B
-      cut_hi = thi;
-      B_cut = B;
-      t = (double)u * zp;
-      if (l == 0) {
-        st.zk = zk;
-        st.cut_lo = tlo;
-        st.cut_hi = thi;
-        st.n_cut_tie = n_tie;
-        st.n_cut_keep = n_keep;
-        st.x_cut = scaled16<DT>(o, T);
-        st.zp = zp;
-        st.n_kept = by_mass ? (int)n_above + n_keep : (int)nk;
-        st.target = t;
-        st.sel_lo = tlo;
-        st.sel_hi = thi;
-        st.sel_n = n_keep;
-        st.sel_rank = (int)fmax(0.0, fmin((w > 0.0) ? floor((t - B) / w) : 0.0, (double)(n_keep - 1)));
-      }
-    } else if (l == 0) {
-      st.sel_lo = tlo;
-      st.sel_hi = thi;
-      st.sel_n = n_tie;
-      st.sel_rank = (int)fmax(0.0, fmin((w > 0.0) ? floor((t - B) / w) : 0.0, (double)(n_tie - 1)));
-    }
-  }
-  if (l == 0) st.kord_lo = kord_lo;
-}
-
 template <int DT, class Src>
-__device__ __forceinline__ void sample_row16(const KArgs& a, Smem& s, Src& src, int b, float T, int kk, float p, float u) {
+__device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, int b, float T, int kk, float p,
+                                             float u) {
   constexpr int EPV = DTraits<DT>::EPV;
   const int V = a.vocab;
+  const int l = lane_id(), wv = wave_id();
 
-  // stream: histogram of ords, row max, NaN flag. The histogram is cleared while the
-  // row's loads are in flight; the barrier orders LDS only.
+  // stream: the histogram. It is cleared while the first loads are in flight; the
+  // barrier orders LDS only.
   {
     u4* h4 = (u4*)s.hist;
-    for (int i = threadIdx.x; i < HIST_WORDS / 4; i += NT) h4[i] = (u4){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < HIST_WORDS / 4 / NT; ++i) h4[i * NT + threadIdx.x] = (u4){0u, 0u, 0u, 0u};
+    if (threadIdx.x == 0) s.nan_cnt = 0u;
   }
   lds_barrier();
-  // packed u16 extremes of the ords: the maximum gives the row max, and NaNs (ords above
-  // +inf or below -inf) show up in either extreme
-  uint32_t pmax = 0u, pmin = 0xffffffffu;
-  src.for_each([&](int, const u4& q, int base, bool vvalid) {
+  src.stream([&](int, const u4& q, int base, bool vvalid) {
     if constexpr (Src::kVector) {
       if (vvalid) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint32_t op = ord16_pair(q[d]);
-          pmax = pk_max_u16(pmax, op);
-          pmin = pk_min_u16(pmin, op);
-          __hip_atomic_fetch_add(&s.hist[(op >> 1) & 0x7fffu], 1u + (op & 1u) * 0xffffu, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
-          __hip_atomic_fetch_add(&s.hist[op >> 17], 1u + ((op >> 16) & 1u) * 0xffffu, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
+        for (int d = 0; d < 4; ++d) hist_add_pair(s, q[d]);
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        if (elem_valid(src, vvalid, base + e)) {
-          const uint32_t o = ord16_pair(elem_raw<DT>(q, e)) & 0xffffu;
-          pmax = max(pmax, o);
-          pmin = min(pmin, 0xffff0000u | o);
-          __hip_atomic_fetch_add(&s.hist[o >> 1], 1u + (o & 1u) * 0xffffu, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-      }
+      for (int e = 0; e < EPV; ++e)
+        if (elem_valid(src, vvalid, base + e)) hist_add_one(s, elem_raw<DT>(q, e));
     }
   });
-  uint32_t omax = max(pmax & 0xffffu, pmax >> 16), omin = min(pmin & 0xffffu, pmin >> 16);
-  omax = wmax_u32(omax);
-  omin = wmin_u32(omin);
-  if (lane_id() == 0) {
-    s.red_i[wave_id()] = (int)omax;
-    s.red_i[NWAVE + wave_id()] = (int)omin;
-  }
   __syncthreads();
+
+  // group counts: thread t sums raws [128t, 128t + 128) (half a group, sixteen 16-byte LDS
+  // reads); the NaN raws sit at the top of each sign's block range
+  {
+    const u4* h4 = (const u4*)s.hist + threadIdx.x * 16;
+    uint32_t c = 0u;
 #pragma unroll
-  for (int w = 0; w < NWAVE; ++w) {
-    omax = max(omax, (uint32_t)s.red_i[w]);
-    omin = min(omin, (uint32_t)s.red_i[NWAVE + w]);
-  }
-  const bool nan = omax > ord16_pos_inf<DT>() || omin < ord16_neg_inf<DT>();
-  const float m = raw_to_float<DT>(raw_of_ord16(omax)) / T;
-  if (nan || !(m > -INFINITY && m < INFINITY)) {
-    if (threadIdx.x == 0) write_error(a, b, nan ? PBS_ROW_NAN : PBS_ROW_NONFINITE, nan ? NAN : m);
-    return;
-  }
-  // -0 was counted under ord 0x7fff (high half of word 0x3fff); merge it into +0 (0x8000,
-  // low half of word 0x4000), so the two zeros form one tie group
-  if (threadIdx.x == 0) {
-    const uint32_t nz = s.hist[0x3fff] >> 16;
-    if (nz) {
-      s.hist[0x3fff] -= nz << 16;
-      s.hist[0x4000] += nz;
+    for (int i = 0; i < 16; ++i) {
+      const u4 qv = h4[i];
+      c += (qv.x & 0xffffu) + (qv.x >> 16);
+      c += (qv.y & 0xffffu) + (qv.y >> 16);
+      c += (qv.z & 0xffffu) + (qv.z >> 16);
+      c += (qv.w & 0xffffu) + (qv.w >> 16);
+    }
+    const uint32_t r0 = threadIdx.x * 128u, inf_raw = DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
+    if ((r0 & 0x7fffu) >= (inf_raw & ~127u) && c) atomicAdd(&s.nan_cnt, c);
+    c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]: the other half of the block
+    if ((l & 1) == 0) {
+      const uint32_t blk = threadIdx.x >> 1;
+      s.gcount[blk < 128u ? blk + 128u : 255u - blk] = c;
     }
   }
   __syncthreads();
 
-  // group summaries. Counts: thread t sums bins [64t, 64t+64) (a quarter group, eight
-  // 16-byte LDS reads), four lanes make a group. Masses: the
-  // non-empty groups only, ranked and dealt round-robin to the waves; lane l weighs bins
-  // 4l..4l+3 of the group.
+  // Every wave checks the total (a u16 counter wraps only if one value occurs more than
+  // 65535 times: the general path takes such rows), then NaN (multinomial raises on it,
+  // sampling.py:27), then finds the row maximum from the highest non-empty ord.
   {
-    const int l = lane_id(), w = wave_id();
-    const u4* h4 = (const u4*)s.hist + threadIdx.x * 8;
     uint32_t c = 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const u4 qv = h4[i];
-      const uint32_t q0 = qv.x, q1 = qv.y, q2 = qv.z, q3 = qv.w;
-      c += (q0 & 0xffffu) + (q0 >> 16) + (q1 & 0xffffu) + (q1 >> 16);
-      c += (q2 & 0xffffu) + (q2 >> 16) + (q3 & 0xffffu) + (q3 >> 16);
-    }
-    c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]
-    c += dpp<0x4e>(c, 0u);  // quad_perm [2,3,0,1]
-    if ((l & 3) == 0) s.gcount[threadIdx.x >> 2] = c;
+    for (int i = 0; i < 4; ++i) c += s.gcount[4 * l + i];
+    if (wsum_u32(c) != (uint32_t)V) return false;
   }
-  __syncthreads();
   {
-    const int l = lane_id(), w = wave_id();
+    const uint32_t inf_raw = DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
+    const uint32_t nan = s.nan_cnt - hist_count_raw(s, inf_raw) - hist_count_raw(s, inf_raw | 0x8000u);
+    if (nan) {
+      if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NAN, NAN);
+      return true;
+    }
+  }
+  Divider dv;
+  dv.init(T);
+  float m;
+  {
+    uint32_t nz = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nz |= (s.gcount[4 * l + i] ? 1u : 0u) << i;
+    const uint64_t any = ballot(nz != 0u);
+    const int L = 63 - __clzll((unsigned long long)any);  // the row is not empty
+    const uint32_t g = 4u * (uint32_t)L + (31u - __clz(bcast_u32(nz, L)));
+    uint32_t n4[4];
+    counts4(s, g * 256u + 4u * (uint32_t)l, n4);
+    uint32_t top = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) top = n4[i] ? (uint32_t)i + 1u : top;
+    const uint64_t any2 = ballot(top != 0u);
+    const int L2 = 63 - __clzll((unsigned long long)any2);
+    const uint32_t omax = g * 256u + 4u * (uint32_t)L2 + bcast_u32(top, L2) - 1u;
+    m = scaled16<DT>(omax, dv);
+  }
+  if (!(m > -INFINITY && m < INFINITY)) {
+    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NONFINITE, m);
+    return true;
+  }
+
+  // group masses: the non-empty groups, ranked and dealt round-robin to the waves; lane l
+  // weighs ords 4l .. 4l+3 of the group
+  {
     uint32_t ne = 0u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) ne |= (s.gcount[4 * l + i] != 0u ? 1u : 0u) << i;
-    if (w == 0) {
+    if (wv == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (!((ne >> i) & 1u)) s.gmass[4 * l + i] = 0.0;
@@ -1232,27 +1284,26 @@ __device__ __forceinline__ void sample_row16(const KArgs& a, Smem& s, Src& src, 
     const uint32_t excl = incl - cnt;
     const uint32_t total = bcast_u32(incl, 63);
 #pragma unroll 1
-    for (uint32_t r = (uint32_t)w; r < total; r += NWAVE) {
+    for (uint32_t r = (uint32_t)wv; r < total; r += NWAVE) {
       const bool mine = r >= excl && r < incl;
       const int L = first_lane(ballot(mine));
       // only the owning lane's rank is meaningful (and bounded by its popcount, <= 4)
       uint32_t bits = ne;
       for (uint32_t k = mine ? r - excl : 0u; k > 0u; --k) bits &= bits - 1u;
       const uint32_t g = bcast_u32(4u * (uint32_t)l + (uint32_t)(__ffs(bits) - 1), L);
-      const uint32_t w0 = s.hist[g * 128u + 2u * l], w1 = s.hist[g * 128u + 2u * l + 1u];
-      const uint32_t n[4] = {w0 & 0xffffu, w0 >> 16, w1 & 0xffffu, w1 >> 16};
+      uint32_t n4[4];
+      counts4(s, g * 256u + 4u * (uint32_t)l, n4);
       double part = 0.0;
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (n[k]) part += (double)n[k] * weight16<DT>(g * 256u + 4u * l + (uint32_t)k, T, m);
+        if (n4[k]) part += (double)n4[k] * weight16<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
       part = wsum_f64(part);
       if (l == 0) s.gmass[g] = part;
     }
   }
   __syncthreads();
-  if (wave_id() == 0) {
+  if (wv == 0) {
     // top-down exclusive prefixes: lane l holds groups 255-4l .. 252-4l
-    const int l = lane_id();
     uint32_t c[4];
     double w[4];
 #pragma unroll
@@ -1264,10 +1315,8 @@ __device__ __forceinline__ void sample_row16(const KArgs& a, Smem& s, Src& src, 
     const double wt = ((w[0] + w[1]) + w[2]) + w[3];
     const uint32_t ci = wscan_u32(ct);
     const double wi = wscan_f64(wt);
-    double we = __shfl_up(wi, 1);
-    if (l == 0) we = 0.0;
     uint32_t rc = ci - ct;
-    double rw = we;
+    double rw = wi - wt;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       s.gabove_cnt[255 - 4 * l - i] = rc;
@@ -1277,49 +1326,26 @@ __device__ __forceinline__ void sample_row16(const KArgs& a, Smem& s, Src& src, 
     }
   }
   __syncthreads();
-  if (wave_id() == 0) {
-    // wave 0's slice of a register-resident row goes to LDS while it resolves, so the
-    // searches get the registers the row occupies
-    if constexpr (Src::kStore) {
-      static_assert(sizeof(s.park) >= sizeof(src.r[0]) * 64 * (sizeof(src.r) / sizeof(src.r[0])) ||
-                        (sizeof(src.r) / sizeof(src.r[0])) > PARK_CHUNKS,
-                    "park area");
-      if constexpr ((sizeof(src.r) / sizeof(src.r[0])) <= PARK_CHUNKS) {
-        constexpr int NC = sizeof(src.r) / sizeof(src.r[0]);
-#pragma unroll
-        for (int j = 0; j < NC; ++j) s.park[j * 64 + lane_id()] = src.r[j];
-        // the compiler must not forward the parked values past the search (that would
-        // keep the row live in registers after all)
-        asm volatile("" ::: "memory");
-        resolve16<DT>(s, V, T, kk, p, u, m);
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < NC; ++j) src.r[j] = s.park[j * 64 + lane_id()];
-      } else {
-        resolve16<DT>(s, V, T, kk, p, u, m);
-      }
-    } else {
-      resolve16<DT>(s, V, T, kk, p, u, m);
-    }
+  if (wv == 0) {
+    if (!resolve16<DT>(s, V, dv, kk, p, u, m) && l == 0) s.st.status = -1;
   }
   __syncthreads();
   const RowState st = s.st;
   __syncthreads();
-  if (st.status != PBS_ROW_OK) {
-    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NONFINITE, m);
-    return;
-  }
+  if (st.status != PBS_ROW_OK) return false;  // a counter wrapped: general path
 
   // which of the tied tokens: the sel_rank-th lowest index with ord in [sel_lo, sel_hi]
   const int tok = select_tied16<DT>(src, s, st.sel_lo, st.sel_hi, st.sel_rank);
   if (threadIdx.x == 0) write_info(a, b, tok < 0 ? 0 : tok, PBS_ROW_OK, st);
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------
-// fp32 stochastic row: exact bisection on 32-bit ords of the scaled values.
-// Every probe is one pass over the row with fp64 accumulation in a fixed order, so the
-// result is deterministic. Register-resident rows keep x = v/T in place after the first
-// pass; rows streamed from memory redo the (exact) division on every pass.
+// General stochastic row (fp32 logits, and 16-bit rows whose histogram counters would
+// wrap): exact bisection on 32-bit ords of x = fp32(v)/T. Every probe is one pass over
+// the row with fp64 accumulation in a fixed order, so the result is deterministic. The
+// first pass streams `src0` (registers when the row fits); the bisection passes re-read
+// the row (`src`), redoing the exact division per element.
 // ---------------------------------------------------------------------------------------
 
 // exp(x - m) for fp32 x <= m: the difference and the scaling by log2(e) in fp64, the
@@ -1333,27 +1359,24 @@ __device__ __forceinline__ float weight32(float x, float m) {
   return ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
 }
 
-template <class Src>
-__device__ __forceinline__ float x_of(const Divider& dv, uint32_t raw) {
-  if constexpr (Src::kStore) {
-    return __uint_as_float(raw);
-  } else {
-    return dv(__uint_as_float(raw));
-  }
+template <int DT>
+__device__ __forceinline__ float x_at(const Divider& dv, const u4& q, int e) {
+  return dv(raw_to_float<DT>(elem_raw<DT>(q, e)));
 }
 
 // count and mass (relative to m) of elements with ord32(x) >= t
-template <class Src>
-__device__ __forceinline__ void f32_ge(const Src& src, Smem& s, const Divider& dv, uint32_t t, float m, bool want_mass,
-                       uint32_t& cnt, double& mass) {
+template <int DT, class Src>
+__device__ __forceinline__ void bis_ge(const Src& src, Smem& s, const Divider& dv, uint32_t t, float m,
+                                       bool want_mass, uint32_t& cnt, double& mass) {
+  constexpr int EPV = DTraits<DT>::EPV;
   uint32_t c = 0;
   double ms = 0.0;
   src.for_each([&](int, const u4& q, int base, bool vvalid) {
     float part = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < EPV; ++e) {
       if (elem_valid(src, vvalid, base + e)) {
-        const float x = x_of<Src>(dv, q[e]);
+        const float x = x_at<DT>(dv, q, e);
         if (ord32(x) >= t) {
           ++c;
           if (want_mass) part += weight32(x, m);
@@ -1382,55 +1405,58 @@ __device__ __forceinline__ void f32_ge(const Src& src, Smem& s, const Divider& d
 }
 
 // largest o in [lo, hi] with count(ord >= o) >= need; count(ord >= lo) >= need is given
-template <class Src>
-__device__ __forceinline__ uint32_t f32_bisect_count(const Src& src, Smem& s, const Divider& dv, uint32_t lo, uint32_t hi,
-                                     uint32_t need) {
+template <int DT, class Src>
+__device__ __forceinline__ uint32_t bis_count(const Src& src, Smem& s, const Divider& dv, uint32_t lo, uint32_t hi,
+                                              uint32_t need) {
   while (lo < hi) {
     const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) / 2);
     uint32_t c;
     double ms;
-    f32_ge(src, s, dv, mid, 0.0f, false, c, ms);
+    bis_ge<DT>(src, s, dv, mid, 0.0f, false, c, ms);
     if (c >= need) lo = mid; else hi = mid - 1;
   }
   return lo;
 }
 
 // largest o in [lo, hi] with mass(ord >= o) > target; mass(ord >= lo) > target is given
-template <class Src>
-__device__ __forceinline__ uint32_t f32_bisect_mass(const Src& src, Smem& s, const Divider& dv, uint32_t lo, uint32_t hi,
-                                    double target, float m) {
+template <int DT, class Src>
+__device__ __forceinline__ uint32_t bis_mass(const Src& src, Smem& s, const Divider& dv, uint32_t lo, uint32_t hi,
+                                             double target, float m) {
   while (lo < hi) {
     const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) / 2);
     uint32_t c;
     double ms;
-    f32_ge(src, s, dv, mid, m, true, c, ms);
+    bis_ge<DT>(src, s, dv, mid, m, true, c, ms);
     if (ms > target) lo = mid; else hi = mid - 1;
   }
   return lo;
 }
 
-// The first pass reads `src0` (registers when resident); the bisection passes re-stream
-// the row from memory (`src`), so no register copy of the row stays live across them.
-template <class Src0, class Src>
-__device__ __forceinline__ void sample_row32(const KArgs& a, Smem& s, const Src0& src0, const Src& src, int b,
-                                             float T, int kk, float p, float u) {
-  const int V = a.vocab;
-  Divider dv;
-  dv.init(T);
-  // stream: max of x = v/T, NaN flag
+// First pass over the row: max of x and the NaN flag (returns NaN then).
+template <int DT, class Src>
+__device__ __forceinline__ float bis_max(Src& src, Smem& s, const Divider& dv, bool streaming) {
+  constexpr int EPV = DTraits<DT>::EPV;
   float xmax = -INFINITY;
   int nan = 0;
-  src0.for_each([&](int, const u4& q, int base, bool vvalid) {
+  auto f = [&](int, const u4& q, int base, bool vvalid) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x = dv(__uint_as_float(q[e]));
-      if (elem_valid(src0, vvalid, base + e)) {
+    for (int e = 0; e < EPV; ++e) {
+      const float x = x_at<DT>(dv, q, e);
+      if (elem_valid(src, vvalid, base + e)) {
         xmax = fmaxf(xmax, x);
         nan |= (x != x) ? 1 : 0;
       }
     }
-  });
-  const float m = block_max_nan(xmax, nan, s);
+  };
+  if (streaming) src.stream(f);
+  else src.for_each(f);
+  return block_max_nan(xmax, nan, s);
+}
+
+template <int DT, class Src>
+__device__ __forceinline__ void sample_row_bisect(const KArgs& a, Smem& s, const Src& src, int b, float m,
+                                                  const Divider& dv, int kk, float p, float u) {
+  const int V = a.vocab;
   if (m != m || !(m > -INFINITY && m < INFINITY)) {
     if (threadIdx.x == 0) write_error(a, b, m != m ? PBS_ROW_NAN : PBS_ROW_NONFINITE, m);
     return;
@@ -1446,11 +1472,11 @@ __device__ __forceinline__ void sample_row32(const KArgs& a, Smem& s, const Src0
   // top-k: kord = k-th largest ord
   uint32_t kord = ord_lo;
   if (kk > 0 && kk < V) {
-    kord = f32_bisect_count(src, s, dv, ord_lo, ord_m, (uint32_t)kk);
+    kord = bis_count<DT>(src, s, dv, ord_lo, ord_m, (uint32_t)kk);
     st.x_kth = float_of_ord32(kord);
   }
   st.kord_lo = kord;
-  f32_ge(src, s, dv, kord, m, true, c, ms);
+  bis_ge<DT>(src, s, dv, kord, m, true, c, ms);
   const double zk = ms;
   const uint32_t nk = c;
   st.zk = zk;
@@ -1460,10 +1486,10 @@ __device__ __forceinline__ void sample_row32(const KArgs& a, Smem& s, const Src0
   double above_cut;
   if (p < 1.0f && zk * (double)p < zk) {
     const double tau = (double)p * zk;
-    cut = f32_bisect_mass(src, s, dv, kord, ord_m, tau, m);
+    cut = bis_mass<DT>(src, s, dv, kord, ord_m, tau, m);
     uint32_t n_above, n_ge;
-    f32_ge(src, s, dv, cut + 1u, m, true, n_above, above_cut);
-    f32_ge(src, s, dv, cut, m, false, n_ge, ms);
+    bis_ge<DT>(src, s, dv, cut + 1u, m, true, n_above, above_cut);
+    bis_ge<DT>(src, s, dv, cut, m, false, n_ge, ms);
     st.n_cut_tie = (int)(n_ge - n_above);
     const double w = (double)weight32(float_of_ord32(cut), m);
     double kf = (w > 0.0) ? floor((tau - above_cut) / w) + 1.0 : (double)st.n_cut_tie;
@@ -1473,9 +1499,9 @@ __device__ __forceinline__ void sample_row32(const KArgs& a, Smem& s, const Src0
     st.n_kept = (int)n_above + st.n_cut_keep;
   } else {
     // keep all of K: the cutoff group is K's lowest value
-    cut = f32_bisect_count(src, s, dv, kord, ord_m, nk);
+    cut = bis_count<DT>(src, s, dv, kord, ord_m, nk);
     uint32_t n_above;
-    f32_ge(src, s, dv, cut + 1u, m, true, n_above, above_cut);
+    bis_ge<DT>(src, s, dv, cut + 1u, m, true, n_above, above_cut);
     st.n_cut_tie = (int)(nk - n_above);
     st.n_cut_keep = st.n_cut_tie;
     st.zp = zk;
@@ -1491,11 +1517,11 @@ __device__ __forceinline__ void sample_row32(const KArgs& a, Smem& s, const Src0
   uint32_t sel = cut;
   int rank;
   if (t < above_cut) {
-    sel = f32_bisect_mass(src, s, dv, cut + 1u, ord_m, t, m);
+    sel = bis_mass<DT>(src, s, dv, cut + 1u, ord_m, t, m);
     double B;
     uint32_t n_above, n_ge;
-    f32_ge(src, s, dv, sel + 1u, m, true, n_above, B);
-    f32_ge(src, s, dv, sel, m, false, n_ge, ms);
+    bis_ge<DT>(src, s, dv, sel + 1u, m, true, n_above, B);
+    bis_ge<DT>(src, s, dv, sel, m, false, n_ge, ms);
     const double w = (double)weight32(float_of_ord32(sel), m);
     const double rf = (w > 0.0) ? floor((t - B) / w) : 0.0;
     rank = (int)fmax(0.0, fmin(rf, (double)((int)(n_ge - n_above) - 1)));
@@ -1504,9 +1530,8 @@ __device__ __forceinline__ void sample_row32(const KArgs& a, Smem& s, const Src0
     const double rf = (w > 0.0) ? floor((t - above_cut) / w) : 0.0;
     rank = (int)fmax(0.0, fmin(rf, (double)(st.n_cut_keep - 1)));
   }
-  const int tok = select_index<PBS_DTYPE_F32>(src, s, [&](uint32_t raw) {
-    return ord32(x_of<Src>(dv, raw)) == sel;
-  }, rank);
+  const int tok = select_index<DT>(src, s, [&](uint32_t raw) { return ord32(dv(raw_to_float<DT>(raw))) == sel; },
+                                   rank);
 
   if (threadIdx.x == 0) write_info(a, b, tok < 0 ? 0 : tok, PBS_ROW_OK, st);
 }
@@ -1539,7 +1564,7 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
     float bv = -INFINITY;
     int bi = INT32_MAX;
     int nan_i = INT32_MAX;
-    src.for_each([&](int, const u4& q, int base, bool vvalid) {
+    src.stream([&](int, const u4& q, int base, bool vvalid) {
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
         const float v = raw_to_float<DT>(elem_raw<DT>(q, e));
@@ -1566,14 +1591,28 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
     }
     return;
   }
-  if constexpr (B16) {
-    sample_row16<DT>(a, s, src, b, T, kk, p, u);
-  } else if constexpr (Src::kVector) {
+  Divider dv;
+  dv.init(T);
+  if constexpr (Src::kVector) {
+    // The bisection passes re-read the row, so no register copy of it stays live across
+    // them. 16-bit rows get here only when a histogram counter wrapped (one value more
+    // than 65535 times); their first pass re-reads the row as well.
     MemRow<DT> mem;
     mem.init((const uint8_t*)a.logits + (size_t)lrow * (size_t)a.row_stride * elt, a.nvec, a.vocab);
-    sample_row32(a, s, src, mem, b, T, kk, p, u);
+    float m;
+    if constexpr (B16) {
+      if (sample_row16<DT>(a, s, src, b, T, kk, p, u)) return;
+      m = bis_max<DT>(mem, s, dv, false);
+    } else {
+      m = bis_max<DT>(src, s, dv, true);
+    }
+    sample_row_bisect<DT>(a, s, mem, b, m, dv, kk, p, u);
   } else {
-    sample_row32(a, s, src, src, b, T, kk, p, u);
+    if constexpr (B16) {
+      if (sample_row16<DT>(a, s, src, b, T, kk, p, u)) return;
+    }
+    const float m = bis_max<DT>(src, s, dv, !B16);
+    sample_row_bisect<DT>(a, s, src, b, m, dv, kk, p, u);
   }
 }
 
@@ -1684,6 +1723,8 @@ int launch_dt(const pbs::KArgs& a, int64_t rows, bool vec, hipStream_t stream) {
     else if (nch <= 8) hipLaunchKernelGGL((k_sample<DT, 8>), grid, block, 0, stream, a);
     else if (nch <= 12) hipLaunchKernelGGL((k_sample<DT, 12>), grid, block, 0, stream, a);
     else if (nch <= 16) hipLaunchKernelGGL((k_sample<DT, 16>), grid, block, 0, stream, a);
+    else if (nch <= 24) hipLaunchKernelGGL((k_sample<DT, 24>), grid, block, 0, stream, a);
+    else if (nch <= 32) hipLaunchKernelGGL((k_sample<DT, 32>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((k_sample<DT, 0>), grid, block, 0, stream, a);
   }
   if (a.out_probs || a.out_kept) {
