@@ -36,7 +36,7 @@ constexpr int NT = 512;            // threads per workgroup: one workgroup per r
 constexpr int NWAVE = NT / 64;     // wave64
 constexpr int HIST_WORDS = 32768;  // 64K packed u16 counters = 128 KB of LDS
 constexpr int NGROUP = 256;        // histogram groups of 256 ords (high byte of a 16-bit ord)
-constexpr int PIPE = 16;           // 16-byte loads per thread in flight while a row streams in
+constexpr int PIPE = 4;            // 16-byte loads per thread in flight while a row streams in
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -179,15 +179,15 @@ __device__ __forceinline__ double exp_neg(double d) {
   return ldexp(q, (int)n);
 }
 
-// exp(x - m) for fp32 x <= m: the difference and its scaling by log2(e) in fp64, the
-// fractional power of two (|f| <= 1/2) on the hardware exp2, the integer power exact.
-// Relative error about 1.5e-7; deterministic.
+// exp(x - m) for fp32 x <= m, in fp32 on the hardware exp2: exp2(RN(RN(x - m) * log2 e)).
+// The roundings of the difference and the product perturb the exponent by at most
+// 2^-23 |x - m|, so the error relative to the largest weight (1, at x = m) stays below
+// max(e^-d * d) * 2^-23 ~ 5e-8 plus the exp2 error of about one ulp: far inside the
+// tolerances on probabilities (1e-5) and on CDF boundaries (1e-6 of the total mass).
+// Deterministic; returned in fp64 for the sums.
 __device__ __forceinline__ double weight_f(float x, float m) {
   if (!(x > -INFINITY)) return 0.0;
-  double t = ((double)x - (double)m) * 1.4426950408889634074;
-  t = fmax(t, -1100.0);
-  const double n = rint(t);
-  return ldexp((double)__builtin_amdgcn_exp2f((float)(t - n)), (int)n);
+  return (double)__builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -267,6 +267,10 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t ord16_pair(uint32_t w) {
   const s16x2 sg = __builtin_bit_cast(s16x2, w) >> (s16x2){15, 15};
   return w ^ (__builtin_bit_cast(uint32_t, sg) | 0x80008000u);
+}
+// acc + low half + high half of w (one v_dot2_u32_u16)
+__device__ __forceinline__ uint32_t add_u16_pair(uint32_t w, uint32_t acc) {
+  return __builtin_amdgcn_udot2(__builtin_bit_cast(u16x2, w), (u16x2){1, 1}, acc, false);
 }
 __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
@@ -360,10 +364,12 @@ struct __align__(16) Smem {
   uint32_t gabove_cnt[NGROUP];   // count strictly above the group (descending order)
   double gmass[NGROUP];          // fp64 mass of each group
   double gabove_mass[NGROUP];    // mass strictly above the group
+  double submass[NGROUP * 8];    // mass of each subgroup of 32 ords (16-bit rows)
   double red_d[NWAVE];
   float red_f[NWAVE];
   int red_i[2 * NWAVE];
   uint32_t nan_cnt;              // 16-bit rows: elements in the NaN / inf raw blocks
+
   int sel_jstar, sel_rank, sel_index;
   RowState st;
 };
@@ -674,9 +680,9 @@ __device__ __forceinline__ int select_index(const Src& src, Smem& s, M&& match, 
 // Index selection for register-resident 16-bit rows: the rank-th lowest-index element
 // whose key lies in [lo, lo + span]. The key is the raw 16-bit pattern (ORD = false: a
 // range of values of one sign is a contiguous range of raws) or the unfolded ord (ORD =
-// true: ranges that take in both -0 and +0). Per-(chunk, wave) match counts come from
-// ballots of the per-element compares (scalar popcounts, skipped where the wave has no
-// match in the chunk); only the wave holding the answer then looks at its lanes.
+// true: ranges that take in both -0 and +0). Per-(chunk, wave) match counts locate the
+// answer (exact counts only where a wave has a match in the chunk); only the wave holding
+// it then looks at its lanes.
 __device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
 }
@@ -704,25 +710,32 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
   static_assert(NCH * NWAVE <= 256, "chunk table must fit 4 entries per lane");
   const int l = lane_id(), w = wave_id();
   const uint32_t lo2 = lo | (lo << 16);
+  const u16x2 lo2v = __builtin_bit_cast(u16x2, lo2);
+  const u16x2 span2v = __builtin_bit_cast(u16x2, span | (span << 16));
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
-    const bool vv = j * NT + (int)threadIdx.x < src.nvec;
-    uint64_t mk[8];
-    uint64_t any = 0;
+    const uint64_t vmask = ballot(j * NT + (int)threadIdx.x < src.nvec);
+    // Does any of the lane's 8 elements match? key - lo (mod 2^16) <= span is a zero after
+    // a saturating subtraction of span; the minimum over the halves finds one. About
+    // three packed VALU ops per 16-bit pair, one compare per chunk, no scalar chains.
+    u16x2 mn = {0xffffu, 0xffffu};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t dl = pk_sub_u16(key16x2<ORD>(src.r[j][d]), lo2);
-      mk[2 * d] = ballot(vv && (dl & 0xffffu) <= span);
-      mk[2 * d + 1] = ballot(vv && (dl >> 16) <= span);
-      any |= mk[2 * d] | mk[2 * d + 1];
+      const u16x2 dl = __builtin_bit_cast(u16x2, key16x2<ORD>(src.r[j][d])) - lo2v;
+      mn = __builtin_elementwise_min(mn, __builtin_elementwise_sub_sat(dl, span2v));
     }
+    const uint64_t any = __builtin_amdgcn_uicmp((uint32_t)min(mn.x, mn.y), 0u, 32 /* eq */) & vmask;
     uint32_t c = 0;
     if (any) {
+      // rare: the exact count of this chunk's matches in the wave
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c += (uint32_t)__popcll(mk[e]);
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t dl = pk_sub_u16(key16x2<ORD>(src.r[j][d]), lo2);
+        c += (uint32_t)__popcll(__builtin_amdgcn_uicmp(dl & 0xffffu, span, 37 /* ule */) & vmask);
+        c += (uint32_t)__popcll(__builtin_amdgcn_uicmp(dl >> 16, span, 37 /* ule */) & vmask);
+      }
     }
     if (l == 0) s.hist[j * NWAVE + w] = c;
-    __builtin_amdgcn_sched_barrier(0);  // one chunk's masks live at a time
   }
   __syncthreads();
   if (w == 0) {
@@ -874,12 +887,18 @@ __device__ __forceinline__ double weight16(uint32_t o, const Divider& dv, float 
   return weight_f(scaled16<DT>(o, dv), m);
 }
 
-// Ords whose scaled value equals that of ord o. Distinct 16-bit values only meet after the
-// division by T at the under/overflow ends (and -0 meets +0); the map is monotone, so
-// binary search.
+// Ords whose scaled value equals that of ord o. Neighbouring 16-bit values differ by at
+// least 2^-11 relative, far more than fp32 rounding, so they only meet after the division
+// by T where the quotient is subnormal, zero or infinite (-0 meets +0 there too); the map
+// is monotone, so binary search.
 template <int DT>
 __device__ __forceinline__ void tie_range16(uint32_t o, const Divider& dv, uint32_t& lo, uint32_t& hi) {
   const float x = scaled16<DT>(o, dv);
+  const float ax = fabsf(x);
+  if (ax >= 1.17549435e-38f && ax <= 3.40282347e38f) {
+    lo = hi = o;
+    return;
+  }
   uint32_t a = ord16_neg_inf<DT>(), b = o;
   if (o <= a || scaled16<DT>(o - 1u, dv) < x) {
     a = o;
@@ -904,75 +923,173 @@ __device__ __forceinline__ void tie_range16(uint32_t o, const Divider& dv, uint3
 }
 
 // ---------------------------------------------------------------------------------------
-// searches over one group, run by one wave. Lane l holds the four ords
-// g*256 + 255 - 4l - i (i = 0..3), i.e. the group in descending order.
+// searches. Wave-local: every wave runs them on the same LDS state and gets the same
+// answer, so they need no barrier. Three levels, in descending ord order: groups of 256
+// ords (count and mass prefix tables), subgroups of 32 ords (masses written by the mass
+// pass; their prefixes are summed here, sequentially, in the same order the group mass
+// was) and single ords (weights computed on the spot).
 // ---------------------------------------------------------------------------------------
-struct GroupHit {
-  uint32_t o;         // the ord found
-  uint32_t cnt_excl;  // elements of the group above o (ords in range only)
-  double mass_excl;   // their mass
-  uint32_t cnt;       // elements at o
+struct BinHit {
+  uint32_t o;          // the ord found
+  uint32_t cnt;        // elements at o
+  uint32_t cnt_above;  // elements above o
+  double mass_above;   // their mass
+  double w;            // weight of one element at o
 };
 
-// BY_MASS: the first ord >= lo (descending) whose inclusive mass from the group top exceeds
-// `target`; if rounding keeps every cumulative at or below it, the lowest non-empty ord >= lo.
-// Otherwise: the first ord >= lo whose inclusive count reaches `need`. Either way the
-// count and mass of the group's elements above the ord come with it.
-template <int DT, bool BY_MASS>
-__device__ __forceinline__ GroupHit group_search(const Smem& s, uint32_t g, uint32_t lo, const Divider& dv, float m,
-                                                 uint32_t need, double target) {
+// the lowest non-empty group (latest in descending order) whose elements start at or
+// before the need-th one: the group holding it
+__device__ __forceinline__ int find_group_count(const Smem& s, uint32_t need) {
   const int l = lane_id();
-  uint32_t n4[4];
-  counts4(s, g * 256u + 252u - 4u * (uint32_t)l, n4);
-  uint32_t c[4];
-  double w[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t o = g * 256u + 255u - 4u * (uint32_t)l - (uint32_t)i;
-    c[i] = (o >= lo) ? n4[3 - i] : 0u;
-    if (c[i]) w[i] = (double)c[i] * weight16<DT>(o, dv, m);
-  }
-  const uint32_t ct = c[0] + c[1] + c[2] + c[3];
-  const uint32_t ci = wscan_u32(ct);
-  const double wt = ((w[0] + w[1]) + w[2]) + w[3];
-  const double wi = wscan_f64(wt);
-  uint64_t hit = BY_MASS ? ballot(wi > target) : ballot(ci >= need);
-  bool last = false;
-  if (!hit) {
-    hit = ballot(ct != 0u);
-    last = true;
-  }
-  // (an empty range cannot reach here from the searches below; lane 0 keeps it in bounds)
-  const int L = !hit ? 0 : last ? 63 - __clzll((unsigned long long)hit) : first_lane(hit);
-  uint32_t rc = ci - ct;
-  double rw = wi - wt;
   int found = -1;
-  uint32_t fc = 0u;
-  double fw = 0.0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bool take;
-    if (last) take = c[i] != 0u;  // keeps the lowest non-empty one
-    else if (BY_MASS) take = found < 0 && rw + w[i] > target;
-    else take = found < 0 && rc + c[i] >= need;
-    if (take) {
-      found = i;
-      fc = rc;
-      fw = rw;
-    }
-    rc += c[i];
-    rw += w[i];
+  for (int i = 3; i >= 0; --i) {
+    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
+    if (s.gcount[g] && s.gabove_cnt[g] < need) found = (int)g;
   }
-  if (found < 0) found = 3;
-  GroupHit h;
-  h.o = g * 256u + 255u - bcast_u32(4u * (uint32_t)l + (uint32_t)found, L);
-  h.cnt_excl = bcast_u32(fc, L);
-  h.mass_excl = bcast_f64(fw, L);
-  h.cnt = bcast_u32(c[found], L);
-  return h;
+  // lanes hold ascending groups: the first lane with a hit has the lowest
+  const uint64_t hit = ballot(found >= 0);
+  return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
 }
 
-// count and mass of the elements with ord >= t (whole wave)
+// the lowest group >= lo >> 8 with mass, whose mass starts at or before target: the group
+// holding it (a target that rounding puts past the group's end falls to its lowest element)
+__device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, double target) {
+  const int l = lane_id();
+  const uint32_t glo = lo >> 8;
+  int found = -1;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
+    if (g >= glo && s.gmass[g] > 0.0 && s.gabove_mass[g] <= target) found = (int)g;
+  }
+  const uint64_t hit = ballot(found >= 0);
+  return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
+}
+
+// elements of group g with ord > o (4 ords per lane)
+__device__ __forceinline__ uint32_t count_above_in_group(const Smem& s, uint32_t g, uint32_t o) {
+  const int l = lane_id();
+  uint32_t n4[4];
+  counts4(s, g * 256u + 4u * (uint32_t)l, n4);
+  uint32_t c = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c += (g * 256u + 4u * (uint32_t)l + (uint32_t)i > o) ? n4[i] : 0u;
+  return wsum_u32(c);
+}
+
+// the need-th element (descending) of group g: its ord, count and the count above it
+__device__ __forceinline__ void bins_count(const Smem& s, uint32_t g, uint32_t need, uint32_t& o, uint32_t& cnt,
+                                           uint32_t& above) {
+  const int l = lane_id();
+  uint32_t n4[4];
+  counts4(s, g * 256u + 252u - 4u * (uint32_t)l, n4);  // lane l: ords 255-4l .. 252-4l
+  const uint32_t ct = n4[0] + n4[1] + n4[2] + n4[3];
+  const uint32_t ci = wscan_u32(ct);
+  const uint64_t hit = ballot(ci >= need);
+  const int L = hit ? first_lane(hit) : 63;
+  uint32_t run = ci - ct;
+  int fi = 0;
+  uint32_t fc = 0u, fa = 0u;
+  bool done = false;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    if (!done && run + n4[i] >= need) {
+      fi = i;
+      fc = n4[i];
+      fa = run;
+      done = true;
+    }
+    run += n4[i];
+  }
+  o = g * 256u + 252u - 4u * (uint32_t)L + bcast_u32((uint32_t)fi, L);
+  cnt = bcast_u32(fc, L);
+  above = bcast_u32(fa, L);
+}
+
+// masses of the subgroups of g above subgroup k, summed from the top in order
+__device__ __forceinline__ double sub_prefix(const Smem& s, uint32_t g, uint32_t k) {
+  double p = 0.0;
+#pragma unroll
+  for (int j = 7; j >= 0; --j)
+    if ((uint32_t)j > k) p += s.submass[g * 8u + (uint32_t)j];
+  return p;
+}
+
+// mass of the elements of subgroup k of g with ord > o, and the weight of ord o
+// (lanes 0..31: one ord each)
+template <int DT>
+__device__ __forceinline__ void mass_above_in_sub(const Smem& s, uint32_t g, uint32_t k, uint32_t o,
+                                                  const Divider& dv, float m, double& mass, double& w) {
+  const int l = lane_id();
+  const uint32_t ol = g * 256u + 32u * k + 31u - (uint32_t)(l & 31);
+  const uint32_t c = (l < 32 && ol > o) ? hist_count(s, ol) : 0u;
+  const double part = c ? (double)c * weight16<DT>(ol, dv, m) : 0.0;
+  mass = wsum_f64(part);
+  w = weight16<DT>(o, dv, m);
+}
+
+// the need-th element (descending) over all ords
+template <int DT>
+__device__ __forceinline__ bool find_by_count(const Smem& s, uint32_t need, const Divider& dv, float m, BinHit& h) {
+  const int g = find_group_count(s, need);
+  if (g < 0) return false;
+  uint32_t ca;
+  bins_count(s, (uint32_t)g, need - s.gabove_cnt[g], h.o, h.cnt, ca);
+  const uint32_t k = (h.o & 255u) >> 5;
+  double ma;
+  mass_above_in_sub<DT>(s, (uint32_t)g, k, h.o, dv, m, ma, h.w);
+  h.cnt_above = s.gabove_cnt[g] + ca;
+  h.mass_above = s.gabove_mass[g] + sub_prefix(s, (uint32_t)g, k) + ma;
+  return true;
+}
+
+// the first ord >= lo (descending) whose cumulative mass from the top exceeds target; if
+// rounding keeps the cumulative at or below it, the lowest ord >= lo with mass there
+template <int DT>
+__device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double target, const Divider& dv, float m,
+                                             BinHit& h) {
+  const int gi = find_group_mass(s, lo, target);
+  if (gi < 0) return false;
+  const uint32_t g = (uint32_t)gi;
+  const double r = target - s.gabove_mass[g];
+  // subgroup: the lowest one in range, non-empty, starting at or before r
+  const uint32_t klo = (g == (lo >> 8)) ? (lo & 255u) >> 5 : 0u;
+  double p = 0.0, start = 0.0;
+  uint32_t k = 8u;
+#pragma unroll
+  for (int j = 7; j >= 0; --j) {
+    const double sm = s.submass[g * 8u + (uint32_t)j];
+    if ((uint32_t)j >= klo && sm > 0.0 && p <= r) {
+      k = (uint32_t)j;
+      start = p;
+    }
+    p += sm;
+  }
+  if (k == 8u) return false;
+  // ords: lanes 0..31, descending
+  const int l = lane_id();
+  const uint32_t ol = g * 256u + 32u * k + 31u - (uint32_t)(l & 31);
+  const uint32_t c = (l < 32 && ol >= lo) ? hist_count(s, ol) : 0u;
+  const double wt = c ? weight16<DT>(ol, dv, m) : 0.0;
+  const double ms = (double)c * wt;
+  const double mi = wscan_f64(ms);
+  uint64_t hit = ballot(l < 32 && start + mi > r);
+  if (!hit) {
+    const uint64_t ne = ballot(ms > 0.0);
+    if (!ne) return false;
+    hit = 1ull << (63 - __clzll((unsigned long long)ne));
+  }
+  const int L = first_lane(hit);
+  h.o = g * 256u + 32u * k + 31u - (uint32_t)L;
+  h.cnt = bcast_u32(c, L);
+  h.w = bcast_f64(wt, L);
+  h.mass_above = s.gabove_mass[g] + start + bcast_f64(mi - ms, L);
+  h.cnt_above = s.gabove_cnt[g] + count_above_in_group(s, g, h.o);
+  return true;
+}
+
+// count and mass of the elements with ord >= t (whole wave; the rare tie-range path)
 template <int DT>
 __device__ __forceinline__ void count_mass_ge(const Smem& s, uint32_t t, const Divider& dv, float m, uint32_t& cnt,
                                               double& mass) {
@@ -999,37 +1116,6 @@ __device__ __forceinline__ void count_mass_ge(const Smem& s, uint32_t t, const D
   mass = wsum_f64(w) + s.gabove_mass[g];
 }
 
-// the group holding the need-th element (descending) among ords >= lo; -1 if none
-__device__ __forceinline__ int find_group_count(const Smem& s, uint32_t lo, uint32_t need) {
-  const int l = lane_id();
-  const uint32_t glo = lo >> 8;
-  int found = -1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
-    const uint32_t ab = s.gabove_cnt[g];
-    if (g >= glo && s.gcount[g] && ab < need && need <= ab + s.gcount[g]) found = (int)g;
-  }
-  const uint64_t hit = ballot(found >= 0);
-  return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
-}
-
-// the group whose cumulative mass interval [above, above + mass) holds target, among
-// groups >= lo >> 8 (the caller makes sure target lies above the range's lower end)
-__device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, double target) {
-  const int l = lane_id();
-  const uint32_t glo = lo >> 8;
-  int found = -1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
-    const double ab = s.gabove_mass[g];
-    if (g >= glo && s.gmass[g] > 0.0 && ab <= target && target < ab + s.gmass[g]) found = (int)g;
-  }
-  const uint64_t hit = ballot(found >= 0);
-  return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
-}
-
 // A tie group located by a search: its ord range, count, mass above it and per-element
 // weight.
 struct TieGroup {
@@ -1041,17 +1127,16 @@ struct TieGroup {
 };
 
 template <int DT>
-__device__ __forceinline__ TieGroup tie_group(const Smem& s, uint32_t g, const GroupHit& h, uint32_t range_lo,
-                                              const Divider& dv, float m) {
+__device__ __forceinline__ TieGroup tie_group(const Smem& s, const BinHit& h, uint32_t range_lo, const Divider& dv,
+                                              float m) {
   TieGroup t;
   tie_range16<DT>(h.o, dv, t.lo, t.hi);
   t.lo = max(t.lo, range_lo);
-  t.w = weight16<DT>(h.o, dv, m);
+  t.w = h.w;
   if (t.lo == h.o && t.hi == h.o) {
     t.n = h.cnt;
-    t.n_above = s.gabove_cnt[g] + h.cnt_excl;
-    // mass above from the group prefix plus the group's own scan
-    t.above = s.gabove_mass[g] + h.mass_excl;
+    t.n_above = h.cnt_above;
+    t.above = h.mass_above;
   } else {
     uint32_t c_ge;
     double m_ge;
@@ -1062,19 +1147,21 @@ __device__ __forceinline__ TieGroup tie_group(const Smem& s, uint32_t g, const G
   return t;
 }
 
-// Top-k threshold, top-p cutoff and draw position from the histogram summaries. Runs on
-// wave 0 only and leaves the result in s.st (written by lane 0). Returns false if a u16
-// counter wrapped (one value more than 65535 times): the caller then takes the general path.
+// Top-k threshold, top-p cutoff and draw position from the histogram summaries. Every
+// wave runs it (the searches are wave-local) and ends with the same RowState. Returns false
+// if a u16 counter wrapped (one value more than 65535 times): the caller then takes the
+// general path.
 template <int DT>
-__device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int kk, float p, float u, float m) {
-  const int l = lane_id();
+__device__ __forceinline__ bool resolve16(const Smem& s, int V, const Divider& dv, int kk, float p, float u, float m,
+                                          bool want_info, RowState& st) {
   const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
   if (total_cnt != (uint32_t)V) return false;
-  RowState st = {};
+  st = RowState{};
   st.status = PBS_ROW_OK;
   st.m = m;
   st.x_kth = -INFINITY;
   const double z_all = s.gabove_mass[0] + s.gmass[0];
+  BinHit h;
 
   // top-k (sampling.py:15-17): K = ords >= the tie group of the k-th largest element
   uint32_t k_lo = 0u;
@@ -1083,44 +1170,33 @@ __device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int
   TieGroup kt = {};
   const bool topk = kk > 0 && kk < V;
   if (topk) {
-    const int g = find_group_count(s, 0u, (uint32_t)kk);
-    if (g < 0) return false;
-    const GroupHit h = group_search<DT, false>(s, (uint32_t)g, 0u, dv, m, (uint32_t)kk - s.gabove_cnt[g], 0.0);
-    kt = tie_group<DT>(s, (uint32_t)g, h, 0u, dv, m);
+    if (!find_by_count<DT>(s, (uint32_t)kk, dv, m, h)) return false;
+    kt = tie_group<DT>(s, h, 0u, dv, m);
     k_lo = kt.lo;
     st.x_kth = scaled16<DT>(h.o, dv);
-    uint32_t c_ge;
-    count_mass_ge<DT>(s, k_lo, dv, m, c_ge, zk);
-    nk = c_ge;
+    zk = kt.above + (double)kt.n * kt.w;
+    nk = kt.n_above + kt.n;
   }
   st.zk = zk;
 
   // top-p (sampling.py:18-25): keep the shortest prefix whose exclusive mass is <= p * Z_K
-  TieGroup ct;
+  TieGroup ct = kt;
   int n_keep;
   double zp;
   const double tau = (double)p * zk;
-  int gc = -1;
-  GroupHit hc = {};
-  if (p < 1.0f) {
-    gc = find_group_mass(s, k_lo, tau);
-    if (gc >= 0) hc = group_search<DT, true>(s, (uint32_t)gc, k_lo, dv, m, 0u, tau - s.gabove_mass[gc]);
-  }
-  if (gc >= 0) {
-    ct = tie_group<DT>(s, (uint32_t)gc, hc, k_lo, dv, m);
+  const bool cut = p < 1.0f && find_by_mass<DT>(s, k_lo, tau, dv, m, h);
+  if (cut) {
+    ct = tie_group<DT>(s, h, k_lo, dv, m);
     const double kf = (ct.w > 0.0) ? floor((tau - ct.above) / ct.w) + 1.0 : (double)ct.n;
     n_keep = (int)fmax(1.0, fmin(kf, (double)ct.n));
     zp = ct.above + (double)n_keep * ct.w;
     st.n_kept = (int)ct.n_above + n_keep;
   } else {
-    // all of K is kept; the cutoff group is K's lowest value
-    if (topk) {
-      ct = kt;
-    } else {
-      const int g = find_group_count(s, 0u, nk);
-      if (g < 0) return false;
-      const GroupHit h = group_search<DT, false>(s, (uint32_t)g, 0u, dv, m, nk - s.gabove_cnt[g], 0.0);
-      ct = tie_group<DT>(s, (uint32_t)g, h, 0u, dv, m);
+    // all of K is kept; the cutoff group is K's lowest value (for the diagnostics only: the
+    // draw below searches all of K)
+    if (!topk && want_info) {
+      if (!find_by_count<DT>(s, nk, dv, m, h)) return false;
+      ct = tie_group<DT>(s, h, 0u, dv, m);
     }
     n_keep = (int)ct.n;
     zp = zk;
@@ -1135,23 +1211,22 @@ __device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int
   st.kord_lo = k_lo;
 
   // draw (sampling.py:26-27, inverse-CDF form): the first kept element whose cumulative
-  // mass exceeds u * Z_P; it lies in the cutoff group unless t < the mass above it
+  // mass exceeds u * Z_P. With a top-p cutoff it lies in the cutoff tie group unless t is
+  // below the mass above that group; without one, anywhere in K.
   const double t = (double)u * zp;
   st.target = t;
   TieGroup dt = ct;
   int n_avail = n_keep;
-  if (t < ct.above) {
-    int g = find_group_mass(s, ct.hi + 1u, t);
-    if (g < 0) g = (int)(ct.hi >> 8);  // rounding at a group edge: search the cutoff's own group
-    const GroupHit h = group_search<DT, true>(s, (uint32_t)g, ct.hi + 1u, dv, m, 0u, t - s.gabove_mass[g]);
-    dt = tie_group<DT>(s, (uint32_t)g, h, ct.hi + 1u, dv, m);
+  if (!cut || t < ct.above) {
+    const uint32_t dlo = cut ? ct.hi + 1u : k_lo;
+    if (!find_by_mass<DT>(s, dlo, t, dv, m, h)) return false;
+    dt = tie_group<DT>(s, h, dlo, dv, m);
     n_avail = (int)dt.n;
   }
   st.sel_lo = dt.lo;
   st.sel_hi = dt.hi;
   st.sel_n = n_avail;
   st.sel_rank = (int)fmax(0.0, fmin((dt.w > 0.0) ? floor((t - dt.above) / dt.w) : 0.0, (double)(n_avail - 1)));
-  if (l == 0) s.st = st;
   return true;
 }
 
@@ -1204,18 +1279,20 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   __syncthreads();
 
   // group counts: thread t sums raws [128t, 128t + 128) (half a group, sixteen 16-byte LDS
-  // reads); the NaN raws sit at the top of each sign's block range
+  // reads, rotated by lane so that a wave's reads spread over the banks); the NaN raws sit
+  // at the top of each sign's block range
   {
     const u4* h4 = (const u4*)s.hist + threadIdx.x * 16;
-    uint32_t c = 0u;
+    uint32_t c0 = 0u, c1 = 0u, c2 = 0u, c3 = 0u;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const u4 qv = h4[i];
-      c += (qv.x & 0xffffu) + (qv.x >> 16);
-      c += (qv.y & 0xffffu) + (qv.y >> 16);
-      c += (qv.z & 0xffffu) + (qv.z >> 16);
-      c += (qv.w & 0xffffu) + (qv.w >> 16);
+      const u4 qv = h4[(i + l) & 15];
+      c0 = add_u16_pair(qv.x, c0);
+      c1 = add_u16_pair(qv.y, c1);
+      c2 = add_u16_pair(qv.z, c2);
+      c3 = add_u16_pair(qv.w, c3);
     }
+    uint32_t c = (c0 + c1) + (c2 + c3);
     const uint32_t r0 = threadIdx.x * 128u, inf_raw = DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
     if ((r0 & 0x7fffu) >= (inf_raw & ~127u) && c) atomicAdd(&s.nan_cnt, c);
     c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]: the other half of the block
@@ -1297,8 +1374,17 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         if (n4[k]) part += (double)n4[k] * weight16<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
-      part = wsum_f64(part);
-      if (l == 0) s.gmass[g] = part;
+      // subgroups of 32 ords are 8-lane segments: quad sums, then row_shr 4 leaves each
+      // segment's sum in its last lane; the group mass sums them top-down in order, as the
+      // searches do
+      part += dpp_f64<0xb1>(part);  // quad_perm [1,0,3,2]
+      part += dpp_f64<0x4e>(part);  // quad_perm [2,3,0,1]
+      part += dpp_f64<ROW_SHR4>(part);
+      if ((l & 7) == 7) s.submass[g * 8u + (uint32_t)(l >> 3)] = part;
+      double gm = 0.0;
+#pragma unroll
+      for (int k = 7; k >= 0; --k) gm += bcast_f64(part, 8 * k + 7);
+      if (l == 0) s.gmass[g] = gm;
     }
   }
   __syncthreads();
@@ -1326,13 +1412,8 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
     }
   }
   __syncthreads();
-  if (wv == 0) {
-    if (!resolve16<DT>(s, V, dv, kk, p, u, m) && l == 0) s.st.status = -1;
-  }
-  __syncthreads();
-  const RowState st = s.st;
-  __syncthreads();
-  if (st.status != PBS_ROW_OK) return false;  // a counter wrapped: general path
+  RowState st;
+  if (!resolve16<DT>(s, V, dv, kk, p, u, m, a.out_info != nullptr, st)) return false;  // a counter wrapped
 
   // which of the tied tokens: the sel_rank-th lowest index with ord in [sel_lo, sel_hi]
   const int tok = select_tied16<DT>(src, s, st.sel_lo, st.sel_hi, st.sel_rank);
