@@ -70,30 +70,42 @@ def copy_only(args, w, torch):
 
 
 def cpu_baseline(w, steps: int, rows: int):
-    """Time the op-for-op CPU restatement of sampling.py (engine.py:133-139 row loop)."""
+    """Time the op-for-op CPU restatement of sampling.py (engine.py:133-139 row loop).
+
+    Runs with every core the process may use (the reported figure) and again with one
+    thread (reported beside it), median over ``steps`` steps each.
+    """
     import torch
 
     from oracle.reference_ops import engine_step_ops
 
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     n = rows or w.rows
     logits = w.logits[:n].contiguous()
     params = [(w.temperature[i], w.top_k[i], w.top_p[i]) for i in range(n)]
-    times = []
-    for s in range(steps):
-        gens = [torch.Generator().manual_seed(1000 * s + i) for i in range(n)]
-        t0 = time.perf_counter()
-        engine_step_ops(logits, params, gens)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+
+    def run(threads, nsteps):
+        torch.set_num_threads(threads)
+        times = []
+        for s in range(nsteps):
+            gens = [torch.Generator().manual_seed(1000 * s + i) for i in range(n)]
+            t0 = time.perf_counter()
+            engine_step_ops(logits, params, gens)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
+
+    med = run(cores, steps)
+    med1 = run(1, max(1, min(steps, 3)))
+    torch.set_num_threads(cores)
     return {
         "value": round(n / med, 3),
         "unit": "rows/s",
         "cores": cores,
         "kind": "port",
         "sample": f"{n} of {w.rows} rows of {w.name}, median of {steps} steps "
-                  f"({med * 1e3:.1f} ms/step, {med / n * 1e3:.2f} ms/row), torch {torch.__version__} CPU",
+                  f"({med * 1e3:.1f} ms/step, {med / n * 1e3:.2f} ms/row), torch {torch.__version__} CPU; "
+                  f"1 thread: {n / med1:.3f} rows/s ({med1 * 1e3:.1f} ms/step)",
+        "value_1_thread": round(n / med1, 3),
     }
 
 
@@ -187,6 +199,22 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
+    # the whole Python surface per engine step: parameter packing, one uniform per
+    # stochastic row from its seeded generator, H2D of the packed parameters, the launch,
+    # D2H of tokens and statuses, and the synchronisation (pagedbatch_amd.sample)
+    from pagedbatch_amd import SamplingParams, sample
+
+    sp = [SamplingParams(temperature=w.temperature[i], top_k=w.top_k[i], top_p=w.top_p[i]) for i in range(rows)]
+    gens = [torch.Generator().manual_seed(i) for i in range(rows)]
+    for i in range(3):
+        sample(bufs[i % copies], sp, gens)
+    e2e = []
+    for i in range(20):
+        t0 = time.perf_counter()
+        sample(bufs[i % copies], sp, gens)
+        e2e.append(time.perf_counter() - t0)
+    e2e_us = statistics.median(e2e) * 1e6
+
     cpu = None
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
@@ -201,6 +229,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 5),
         "us_per_step_kernel": round(kern_ms * 1e3, 3),
+        "us_per_step_python": round(e2e_us, 1),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -153,3 +153,50 @@ def test_nucleus_qwen_fp32_subset(dev):
     rm = list(range(12))
     run_case(dev, w.name + "_subset", w.logits, w.temperature[:12], w.top_k[:12], w.top_p[:12], w.uniform[:12],
              row_map=rm)
+
+
+def test_counter_wrap_takes_general_path(dev):
+    """A 16-bit value occurring more than 65535 times wraps its u16 histogram counter; such
+    rows must go through the general (bisection) path and still match the oracle."""
+    g = torch.Generator().manual_seed(21)
+    V = 131072
+    x = torch.zeros(4, V)
+    x[:, :3000] = torch.randn(4, 3000, generator=g)  # everything else is exactly +0
+    x[1, 5000:] = -0.0                                 # and -0, which ties with +0
+    logits = x.to(torch.bfloat16)
+    T = [1.0, 0.7, 1.3, 0.0]
+    K = [0, 50, 0, 0]
+    P = [0.9, 1.0, 0.5, 1.0]
+    U = [0.99, 0.3, 0.7, 0.0]
+    run_case(dev, "counter_wrap_bf16", logits, T, K, P, U, info_only=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_values_colliding_after_division(dev, dtype):
+    """A huge temperature sends many distinct 16-bit values to the same (subnormal or zero)
+    fp32 quotient: ties that span several histogram bins, including -0 and +0."""
+    g = torch.Generator().manual_seed(22)
+    V = 4096
+    x = torch.randn(6, V, generator=g) * 1e-3
+    x[3:, ::7] = 0.0
+    x[4:, 1::7] = -0.0
+    logits = x.to(dtype)
+    T = [3e36, 1e37, 3e38, 3e36, 1e37, 1e30]
+    K = [0, 10, 0, 100, 0, 5]
+    P = [0.5, 1.0, 0.9, 0.3, 1.0, 0.6]
+    U = [0.1, 0.5, 0.9, 0.25, 0.75, 0.4]
+    run_case(dev, f"collide_{DT_NAME[dtype]}", logits, T, K, P, U)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_register_row_sizes(dev, dtype):
+    """Vocab sizes that land on each register-row width (and just past the largest)."""
+    g = torch.Generator().manual_seed(23)
+    for V in (4096, 8192, 12288, 24576, 49152, 128256, 131072, 151936):
+        x = (torch.randn(8, V, generator=g) * 2.0).to(dtype)
+        T = [0.0, 0.9, 1.0, 1.2] * 2
+        K = [0, 40, 0, V // 3, 1, 0, 7, 0]
+        P = [1.0, 0.9, 0.5, 1.0, 1.0, 0.99, 0.8, 1.0]
+        U = [float(v) for v in torch.rand(8, generator=g)]
+        run_case(dev, f"width_{DT_NAME[dtype]}_{V}", x, T, K, P, U, want_probs=V <= 49152,
+                 info_only=V > 49152)
