@@ -101,6 +101,15 @@ __device__ __forceinline__ double wscan_f64(double v) {
   v += dpp_f64<ROW_BCAST31, 0xc>(v);
   return v;
 }
+__device__ __forceinline__ float wscan_f32(float v) {
+  v += __uint_as_float(dpp<ROW_SHR1>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp<ROW_SHR2>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp<ROW_SHR4>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp<ROW_SHR8>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp<ROW_BCAST15, 0xa>(__float_as_uint(v), 0u));
+  v += __uint_as_float(dpp<ROW_BCAST31, 0xc>(__float_as_uint(v), 0u));
+  return v;
+}
 __device__ __forceinline__ uint32_t wsum_u32(uint32_t v) { return bcast_u32(wscan_u32(v), 63); }
 __device__ __forceinline__ double wsum_f64(double v) { return bcast_f64(wscan_f64(v), 63); }
 
@@ -364,7 +373,7 @@ struct __align__(16) Smem {
   uint32_t gabove_cnt[NGROUP];   // count strictly above the group (descending order)
   double gmass[NGROUP];          // fp64 mass of each group
   double gabove_mass[NGROUP];    // mass strictly above the group
-  double submass[NGROUP * 8];    // mass of each subgroup of 32 ords (16-bit rows)
+  double subabove[NGROUP * 8];   // mass of the subgroups (32 ords) above each one, within its group
   double red_d[NWAVE];
   float red_f[NWAVE];
   int red_i[2 * NWAVE];
@@ -886,6 +895,11 @@ template <int DT>
 __device__ __forceinline__ double weight16(uint32_t o, const Divider& dv, float m) {
   return weight_f(scaled16<DT>(o, dv), m);
 }
+template <int DT>
+__device__ __forceinline__ float weight16f(uint32_t o, const Divider& dv, float m) {
+  const float x = scaled16<DT>(o, dv);
+  return (x > -INFINITY) ? __builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f) : 0.0f;
+}
 
 // Ords whose scaled value equals that of ord o. Neighbouring 16-bit values differ by at
 // least 2^-11 relative, far more than fp32 rounding, so they only meet after the division
@@ -1007,15 +1021,6 @@ __device__ __forceinline__ void bins_count(const Smem& s, uint32_t g, uint32_t n
   above = bcast_u32(fa, L);
 }
 
-// masses of the subgroups of g above subgroup k, summed from the top in order
-__device__ __forceinline__ double sub_prefix(const Smem& s, uint32_t g, uint32_t k) {
-  double p = 0.0;
-#pragma unroll
-  for (int j = 7; j >= 0; --j)
-    if ((uint32_t)j > k) p += s.submass[g * 8u + (uint32_t)j];
-  return p;
-}
-
 // mass of the elements of subgroup k of g with ord > o, and the weight of ord o
 // (lanes 0..31: one ord each)
 template <int DT>
@@ -1024,9 +1029,9 @@ __device__ __forceinline__ void mass_above_in_sub(const Smem& s, uint32_t g, uin
   const int l = lane_id();
   const uint32_t ol = g * 256u + 32u * k + 31u - (uint32_t)(l & 31);
   const uint32_t c = (l < 32 && ol > o) ? hist_count(s, ol) : 0u;
-  const double part = c ? (double)c * weight16<DT>(ol, dv, m) : 0.0;
-  mass = wsum_f64(part);
-  w = weight16<DT>(o, dv, m);
+  const float part = c ? (float)c * weight16f<DT>(ol, dv, m) : 0.0f;
+  mass = (double)bcast_f32(wscan_f32(part), 63);
+  w = (double)weight16f<DT>(o, dv, m);
 }
 
 // the need-th element (descending) over all ords
@@ -1040,7 +1045,7 @@ __device__ __forceinline__ bool find_by_count(const Smem& s, uint32_t need, cons
   double ma;
   mass_above_in_sub<DT>(s, (uint32_t)g, k, h.o, dv, m, ma, h.w);
   h.cnt_above = s.gabove_cnt[g] + ca;
-  h.mass_above = s.gabove_mass[g] + sub_prefix(s, (uint32_t)g, k) + ma;
+  h.mass_above = s.gabove_mass[g] + s.subabove[(uint32_t)g * 8u + k] + ma;
   return true;
 }
 
@@ -1053,39 +1058,44 @@ __device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double 
   if (gi < 0) return false;
   const uint32_t g = (uint32_t)gi;
   const double r = target - s.gabove_mass[g];
-  // subgroup: the lowest one in range, non-empty, starting at or before r
-  const uint32_t klo = (g == (lo >> 8)) ? (lo & 255u) >> 5 : 0u;
-  double p = 0.0, start = 0.0;
-  uint32_t k = 8u;
-#pragma unroll
-  for (int j = 7; j >= 0; --j) {
-    const double sm = s.submass[g * 8u + (uint32_t)j];
-    if ((uint32_t)j >= klo && sm > 0.0 && p <= r) {
-      k = (uint32_t)j;
-      start = p;
-    }
-    p += sm;
-  }
-  if (k == 8u) return false;
-  // ords: lanes 0..31, descending
   const int l = lane_id();
-  const uint32_t ol = g * 256u + 32u * k + 31u - (uint32_t)(l & 31);
+  // subgroup (lanes 0..7, one each): the lowest one in range, with mass, whose interval
+  // [above_k, above_{k-1}) starts at or before r; the intervals tile the group exactly
+  const uint32_t klo = (g == (lo >> 8)) ? (lo & 255u) >> 5 : 0u;
+  const uint32_t kl = (uint32_t)(l & 7);
+  const double st_k = s.subabove[g * 8u + kl];
+  const double en_k = kl ? s.subabove[g * 8u + kl - 1u] : s.gmass[g];
+  const uint64_t ks = ballot(l < 8 && kl >= klo && en_k > st_k && st_k <= r);
+  if (!ks) return false;
+  const int k = first_lane(ks);
+  const double start = bcast_f64(st_k, k);
+  // elements above the subgroup in the group (independent of the bin search below)
+  uint32_t n4[4];
+  counts4(s, g * 256u + 4u * (uint32_t)l, n4);
+  uint32_t ca = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ca += (4 * l + i >= 32 * k + 32) ? n4[i] : 0u;
+  // ords: lanes 0..31, descending; fp32 masses and scan inside one subgroup (its share of
+  // the total is summed in fp64 above)
+  const uint32_t ol = g * 256u + 32u * (uint32_t)k + 31u - (uint32_t)(l & 31);
   const uint32_t c = (l < 32 && ol >= lo) ? hist_count(s, ol) : 0u;
-  const double wt = c ? weight16<DT>(ol, dv, m) : 0.0;
-  const double ms = (double)c * wt;
-  const double mi = wscan_f64(ms);
-  uint64_t hit = ballot(l < 32 && start + mi > r);
+  const float wt = c ? weight16f<DT>(ol, dv, m) : 0.0f;
+  const float ms = (float)c * wt;
+  const float mi = wscan_f32(ms);
+  const uint32_t ci = wscan_u32(c);
+  const float rs = (float)(r - start);
+  uint64_t hit = ballot(l < 32 && mi > rs);
   if (!hit) {
-    const uint64_t ne = ballot(ms > 0.0);
+    const uint64_t ne = ballot(ms > 0.0f);
     if (!ne) return false;
     hit = 1ull << (63 - __clzll((unsigned long long)ne));
   }
   const int L = first_lane(hit);
-  h.o = g * 256u + 32u * k + 31u - (uint32_t)L;
+  h.o = g * 256u + 32u * (uint32_t)k + 31u - (uint32_t)L;
   h.cnt = bcast_u32(c, L);
-  h.w = bcast_f64(wt, L);
-  h.mass_above = s.gabove_mass[g] + start + bcast_f64(mi - ms, L);
-  h.cnt_above = s.gabove_cnt[g] + count_above_in_group(s, g, h.o);
+  h.w = (double)bcast_f32(wt, L);
+  h.mass_above = s.gabove_mass[g] + start + (double)bcast_f32(mi - ms, L);
+  h.cnt_above = s.gabove_cnt[g] + wsum_u32(ca) + bcast_u32(ci - c, L);
   return true;
 }
 
@@ -1370,20 +1380,27 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
       const uint32_t g = bcast_u32(4u * (uint32_t)l + (uint32_t)(__ffs(bits) - 1), L);
       uint32_t n4[4];
       counts4(s, g * 256u + 4u * (uint32_t)l, n4);
-      double part = 0.0;
+      // per-ord masses in fp32 (a u16 count times a weight <= 1), the lane's four summed
+      // in fp32, everything above that in fp64
+      float pf = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (n4[k]) part += (double)n4[k] * weight16<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
+        if (n4[k]) pf += (float)n4[k] * weight16f<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
+      double part = (double)pf;
       // subgroups of 32 ords are 8-lane segments: quad sums, then row_shr 4 leaves each
-      // segment's sum in its last lane; the group mass sums them top-down in order, as the
-      // searches do
+      // segment's sum in its last lane; summed top-down in order, they give the subgroup
+      // prefixes the searches use and the group mass
       part += dpp_f64<0xb1>(part);  // quad_perm [1,0,3,2]
       part += dpp_f64<0x4e>(part);  // quad_perm [2,3,0,1]
       part += dpp_f64<ROW_SHR4>(part);
-      if ((l & 7) == 7) s.submass[g * 8u + (uint32_t)(l >> 3)] = part;
-      double gm = 0.0;
+      // top-down prefixes of the subgroup masses (lane k writes subgroup k's), then the total
+      double gm = 0.0, my_above = 0.0;
 #pragma unroll
-      for (int k = 7; k >= 0; --k) gm += bcast_f64(part, 8 * k + 7);
+      for (int k = 7; k >= 0; --k) {
+        my_above = (l == k) ? gm : my_above;
+        gm += bcast_f64(part, 8 * k + 7);
+      }
+      if (l < 8) s.subabove[g * 8u + (uint32_t)l] = my_above;
       if (l == 0) s.gmass[g] = gm;
     }
   }
