@@ -543,13 +543,29 @@ struct MemRow {
     vocab = vocab_;
   }
   __device__ __forceinline__ void load() {}
+  // Every pass streams the row again: raw buffer loads (range-checked, zeros past the end)
+  // four chunks per step, the next four issued before the current four are used, so eight
+  // loads per thread are in flight instead of one.
   template <class F>
   __device__ __forceinline__ void for_each(F&& f) const {
     const int nch = (nvec + NT - 1) / NT;
-    for (int j = 0; j < nch; ++j) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, nvec * 16, 0x00020000);
+    auto ld = [&](int j) {
+      return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, j * NT * 16, 0));
+    };
+    u4 a0 = ld(0), a1 = ld(1), a2 = ld(2), a3 = ld(3);
+    for (int j = 0; j < nch; j += 4) {
+      const u4 b0 = ld(j + 4), b1 = ld(j + 5), b2 = ld(j + 6), b3 = ld(j + 7);
       const int v = j * NT + (int)threadIdx.x;
-      const u4 q = row[v < nvec ? v : nvec - 1];
-      f(j, q, v * EPV, v < nvec);
+      f(j, a0, v * EPV, v < nvec);
+      if (j + 1 < nch) f(j + 1, a1, (v + NT) * EPV, v + NT < nvec);
+      if (j + 2 < nch) f(j + 2, a2, (v + 2 * NT) * EPV, v + 2 * NT < nvec);
+      if (j + 3 < nch) f(j + 3, a3, (v + 3 * NT) * EPV, v + 3 * NT < nvec);
+      a0 = b0;
+      a1 = b1;
+      a2 = b2;
+      a3 = b3;
     }
   }
   template <class F>
