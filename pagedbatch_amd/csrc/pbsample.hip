@@ -37,6 +37,7 @@ constexpr int NWAVE = NT / 64;     // wave64
 constexpr int HIST_WORDS = 32768;  // 64K packed u16 counters = 128 KB of LDS
 constexpr int NGROUP = 256;        // histogram groups of 256 ords (high byte of a 16-bit ord)
 constexpr int PIPE = 4;            // 16-byte loads per thread in flight while a row streams in
+constexpr int GATHER_CAP = 2048;   // fp32 rows: elements one search window may gather into LDS
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -373,8 +374,16 @@ struct __align__(16) Smem {
   uint32_t gabove_cnt[NGROUP];   // count strictly above the group (descending order)
   double gmass[NGROUP];          // fp64 mass of each group
   double gabove_mass[NGROUP];    // mass strictly above the group
-  double subabove[NGROUP * 8];   // mass of the subgroups (32 ords) above each one, within its group
+  union {
+    double subabove[NGROUP * 8];  // 16-bit rows: mass of the subgroups (32 ords) above each one, in its group
+    uint64_t list[GATHER_CAP];    // fp32 rows: gathered (~key << 32 | index) of one search window
+  };
+  double gmass_hi[NGROUP];       // fp32 rows: upper bounds of the group masses (gmass holds lower bounds)
+  double gabove_hi[NGROUP];
+  uint32_t list_n;               // fp32 rows: entries gathered
+  uint32_t list_hit;             // fp32 rows: result of a list search
   double red_d[NWAVE];
+  double red_d2[NWAVE];
   float red_f[NWAVE];
   int red_i[2 * NWAVE];
   uint32_t nan_cnt;              // 16-bit rows: elements in the NaN / inf raw blocks
@@ -1271,6 +1280,40 @@ __device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t l
   }
 }
 
+// clears the histogram and the NaN counter (every thread takes a share)
+__device__ __forceinline__ void hist_clear(Smem& s) {
+  u4* h4 = (u4*)s.hist;
+#pragma unroll
+  for (int i = 0; i < HIST_WORDS / 4 / NT; ++i) h4[i * NT + threadIdx.x] = (u4){0u, 0u, 0u, 0u};
+  if (threadIdx.x == 0) s.nan_cnt = 0u;
+}
+
+// group counts: thread t sums raws [128t, 128t + 128) (half a group, sixteen 16-byte LDS
+// reads, rotated by lane so that a wave's reads spread over the banks); the elements of the
+// top raw blocks of each sign (inf / NaN of the 16-bit types) also go into s.nan_cnt
+template <int DT>
+__device__ __forceinline__ void hist_group_counts(Smem& s) {
+  const int l = lane_id();
+  const u4* h4 = (const u4*)s.hist + threadIdx.x * 16;
+  uint32_t c0 = 0u, c1 = 0u, c2 = 0u, c3 = 0u;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const u4 qv = h4[(i + l) & 15];
+    c0 = add_u16_pair(qv.x, c0);
+    c1 = add_u16_pair(qv.y, c1);
+    c2 = add_u16_pair(qv.z, c2);
+    c3 = add_u16_pair(qv.w, c3);
+  }
+  uint32_t c = (c0 + c1) + (c2 + c3);
+  const uint32_t r0 = threadIdx.x * 128u, inf_raw = DT == PBS_DTYPE_F16 ? 0x7c00u : 0x7f80u;
+  if ((r0 & 0x7fffu) >= (inf_raw & ~127u) && c) atomicAdd(&s.nan_cnt, c);
+  c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]: the other half of the block
+  if ((l & 1) == 0) {
+    const uint32_t blk = threadIdx.x >> 1;
+    s.gcount[blk < 128u ? blk + 128u : 255u - blk] = c;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // 16-bit stochastic row
 // ---------------------------------------------------------------------------------------
@@ -1283,12 +1326,7 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
 
   // stream: the histogram. It is cleared while the first loads are in flight; the
   // barrier orders LDS only.
-  {
-    u4* h4 = (u4*)s.hist;
-#pragma unroll
-    for (int i = 0; i < HIST_WORDS / 4 / NT; ++i) h4[i * NT + threadIdx.x] = (u4){0u, 0u, 0u, 0u};
-    if (threadIdx.x == 0) s.nan_cnt = 0u;
-  }
+  hist_clear(s);
   lds_barrier();
   src.stream([&](int, const u4& q, int base, bool vvalid) {
     if constexpr (Src::kVector) {
@@ -1304,29 +1342,7 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   });
   __syncthreads();
 
-  // group counts: thread t sums raws [128t, 128t + 128) (half a group, sixteen 16-byte LDS
-  // reads, rotated by lane so that a wave's reads spread over the banks); the NaN raws sit
-  // at the top of each sign's block range
-  {
-    const u4* h4 = (const u4*)s.hist + threadIdx.x * 16;
-    uint32_t c0 = 0u, c1 = 0u, c2 = 0u, c3 = 0u;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const u4 qv = h4[(i + l) & 15];
-      c0 = add_u16_pair(qv.x, c0);
-      c1 = add_u16_pair(qv.y, c1);
-      c2 = add_u16_pair(qv.z, c2);
-      c3 = add_u16_pair(qv.w, c3);
-    }
-    uint32_t c = (c0 + c1) + (c2 + c3);
-    const uint32_t r0 = threadIdx.x * 128u, inf_raw = DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
-    if ((r0 & 0x7fffu) >= (inf_raw & ~127u) && c) atomicAdd(&s.nan_cnt, c);
-    c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]: the other half of the block
-    if ((l & 1) == 0) {
-      const uint32_t blk = threadIdx.x >> 1;
-      s.gcount[blk < 128u ? blk + 128u : 255u - blk] = c;
-    }
-  }
+  hist_group_counts<DT>(s);
   __syncthreads();
 
   // Every wave checks the total (a u16 counter wraps only if one value occurs more than
@@ -1651,6 +1667,603 @@ __device__ __forceinline__ void sample_row_bisect(const KArgs& a, Smem& s, const
 }
 
 // ---------------------------------------------------------------------------------------
+// fp32 stochastic rows.
+//
+// Bins are the top 16 bits of key = ord32(x): 65536 consecutive fp32 values each. The
+// stream histograms them (u16 counters, indexed like the 16-bit rows' raws) and sums the
+// row's softmax mass with a running maximum per thread. From the counts and each bin's
+// value range come a lower and an upper bound on every bin's mass, and so on every
+// cumulative from the top: a search by count lands on one bin; a search by mass lands
+// between the bin where the upper bounds cross the target (the cumulative can cross no
+// earlier) and the bin where the lower bounds do (no later). One more pass gathers those
+// windows' elements into LDS as (~key << 32 | index) and sums the exact mass above each
+// window; sorted ascending (key descending, index ascending), the windows are scanned
+// exactly. Top-k rows whose k-th element lies in the top few thousand gather everything
+// from its bin up and resolve the row from that one list. Rows whose windows hold more
+// elements than LDS takes, or whose counters wrap, take the bisection path.
+// ---------------------------------------------------------------------------------------
+constexpr uint32_t LIST_CAP = HIST_WORDS / 2;  // entries of the list that reuses the histogram
+constexpr uint32_t SMALLK_CAP = 4096;          // top-k rows resolved from one list up to this size
+constexpr float LOG2E_F = 1.44269504088896341f;
+
+// exp(x - m) as the fp32 searches compute it: fp32 difference and product, hardware exp2
+__device__ __forceinline__ float wexp(float x, float m) {
+  return (x > -INFINITY) ? __builtin_amdgcn_exp2f((x - m) * LOG2E_F) : 0.0f;
+}
+// histogram index of x: the top 16 bits of its pattern, -0 folded onto +0 (the raw whose
+// unfolded ord is ord32(x) >> 16)
+__device__ __forceinline__ uint32_t bin_raw32(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return (b == 0x80000000u) ? 0u : (b >> 16);
+}
+__device__ __forceinline__ uint32_t key_of(uint64_t e) { return ~(uint32_t)(e >> 32); }
+__device__ __forceinline__ int index_of(uint64_t e) { return (int)(uint32_t)e; }
+
+// Bounds on wexp(x, m) over the x of bin o that a row with maximum m can hold. wexp is
+// monotone up to its last-ulp rounding; the factors cover that and the fp32 partial sums
+// of the exact passes. The lowest key of the -inf bin is a NaN pattern: weight 0.
+__device__ __forceinline__ void bin_bounds(uint32_t o, float m, float& wlo, float& whi) {
+  const float xlo = float_of_ord32(o << 16);
+  const float xhi = fminf(float_of_ord32((o << 16) | 0xffffu), m);
+  wlo = wexp(xlo, m) * 0.999998f;
+  whi = wexp(xhi, m) * 1.000002f;
+}
+
+// elements in bins >= t (whole wave)
+__device__ __forceinline__ uint32_t count_bins_ge(const Smem& s, uint32_t t) {
+  if (t > 0xffffu) return 0u;
+  const uint32_t g = t >> 8;
+  return count_above_in_group(s, g, t - 1u) + s.gabove_cnt[g];
+}
+
+// The bin >= lo (descending from the top) where the cumulative bound mass, upper bounds
+// (HI) or lower bounds, first exceeds target; the lowest non-empty bin >= lo if it never
+// does. Whole wave, no barrier.
+template <bool HI>
+__device__ __forceinline__ uint32_t find_bin_bound(const Smem& s, uint32_t lo, double target, float m) {
+  const double* above = HI ? s.gabove_hi : s.gabove_mass;
+  const int l = lane_id();
+  const uint32_t glo = lo >> 8;
+  // the lowest non-empty group >= glo whose mass starts at or before target
+  int found = -1, lowest = -1;
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
+    if (g >= glo && s.gcount[g]) {
+      lowest = (int)g;
+      if (above[g] <= target) found = (int)g;
+    }
+  }
+  const uint64_t hit = ballot(found >= 0);
+  int gi;
+  if (hit) {
+    gi = (int)bcast_u32((uint32_t)found, first_lane(hit));
+  } else {
+    const uint64_t any = ballot(lowest >= 0);
+    gi = any ? (int)bcast_u32((uint32_t)lowest, first_lane(any)) : (int)glo;
+  }
+  const uint32_t g = (uint32_t)gi;
+  // lane l: bins 255-4l .. 252-4l of the group, descending
+  uint32_t n4[4];
+  counts4(s, g * 256u + 252u - 4u * (uint32_t)l, n4);
+  double w[4];
+  uint32_t ne = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t o = g * 256u + 255u - 4u * (uint32_t)l - (uint32_t)i;
+    const uint32_t c = (o >= lo) ? n4[3 - i] : 0u;
+    float wl, wh;
+    bin_bounds(o, m, wl, wh);
+    w[i] = (double)c * (double)(HI ? wh : wl);
+    ne |= (c != 0u ? 1u : 0u) << i;
+  }
+  const double wt = ((w[0] + w[1]) + w[2]) + w[3];
+  const double wi = wscan_f64(wt);
+  const double base = above[g];
+  const uint64_t h = ballot(base + wi > target);
+  int L, fi = 0;
+  if (h) {
+    L = first_lane(h);
+    double run = base + (wi - wt);
+    bool done = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!done && run + w[i] > target) {
+        fi = i;
+        done = true;
+      }
+      run += w[i];
+    }
+  } else {
+    const uint64_t nz = ballot(ne != 0u);
+    L = nz ? 63 - __clzll((unsigned long long)nz) : 0;
+    fi = ne ? 31 - __clz(ne) : 0;
+  }
+  return g * 256u + 255u - 4u * (uint32_t)L - bcast_u32((uint32_t)fi, L);
+}
+
+struct Gathered {
+  uint32_t n;     // matches (more than the list's capacity: the list holds only some)
+  uint32_t n1;    // matches in the first window
+  double above1;  // exact mass of the elements (key >= kmin) in bins above hi1
+  double above2;  // ... above hi2
+};
+
+// One pass over the row: every element with key >= kmin whose bin lies in [lo1, hi1] or
+// [lo2, hi2] (either may be empty: lo > hi) goes into L, unsorted.
+template <int DT, class Src>
+__device__ __forceinline__ Gathered gather_bins(const Src& src, Smem& s, uint64_t* L, uint32_t cap,
+                                                const Divider& dv, float m, uint32_t kmin, uint32_t lo1,
+                                                uint32_t hi1, uint32_t lo2, uint32_t hi2) {
+  if (threadIdx.x == 0) s.list_n = 0u;
+  __syncthreads();
+  double acc1 = 0.0, acc2 = 0.0;
+  uint32_t c1 = 0u;
+  src.for_each([&](int, const u4& q, int base, bool vvalid) {
+    float p1 = 0.0f, p2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = x_at<DT>(dv, q, e);
+      const uint32_t key = ord32(x);
+      const uint32_t o = key >> 16;
+      const bool in = elem_valid(src, vvalid, base + e) && key >= kmin;
+      const float w = wexp(x, m);
+      p1 += (in && o > hi1) ? w : 0.0f;
+      p2 += (in && o > hi2) ? w : 0.0f;
+      const bool w1 = o >= lo1 && o <= hi1;
+      if (in && (w1 || (o >= lo2 && o <= hi2))) {
+        const uint32_t slot = atomicAdd(&s.list_n, 1u);
+        if (slot < cap) L[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
+        c1 += w1 ? 1u : 0u;
+      }
+    }
+    acc1 += (double)p1;
+    acc2 += (double)p2;
+  });
+  acc1 = wsum_f64(acc1);
+  acc2 = wsum_f64(acc2);
+  c1 = wsum_u32(c1);
+  if (lane_id() == 0) {
+    s.red_d[wave_id()] = acc1;
+    s.red_d2[wave_id()] = acc2;
+    s.red_i[wave_id()] = (int)c1;
+  }
+  __syncthreads();
+  Gathered r;
+  r.n = s.list_n;
+  r.above1 = 0.0;
+  r.above2 = 0.0;
+  r.n1 = 0u;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    r.above1 += s.red_d[w];
+    r.above2 += s.red_d2[w];
+    r.n1 += (uint32_t)s.red_i[w];
+  }
+  __syncthreads();
+  return r;
+}
+
+// Bitonic sort of L[0, n) ascending (n <= the list's power-of-two capacity), padded with
+// ~0 up to the next power of two. Entries are distinct: the order is unique.
+__device__ __forceinline__ void sort_list(uint64_t* L, uint32_t n) {
+  uint32_t np = 2u;
+  while (np < n) np <<= 1;
+  for (uint32_t i = n + threadIdx.x; i < np; i += NT) L[i] = ~0ull;
+  __syncthreads();
+  for (uint32_t k = 2u; k <= np; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
+      for (uint32_t t = threadIdx.x; t < (np >> 1); t += NT) {
+        const uint32_t i = ((t & ~(j - 1u)) << 1) | (t & (j - 1u));
+        const uint64_t a = L[i], b = L[i | j];
+        if ((a > b) == ((i & k) == 0u)) {
+          L[i] = b;
+          L[i | j] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// first position in [lo, hi) of a sorted list whose entry exceeds v (every thread)
+__device__ __forceinline__ int list_upper(const uint64_t* L, int lo, int hi, uint64_t v) {
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (L[mid] > v) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
+// positions [first, last] of the entries with key `key` in [lo, hi)
+__device__ __forceinline__ void list_key_range(const uint64_t* L, int lo, int hi, uint32_t key, int& first,
+                                               int& last) {
+  const uint64_t v = (uint64_t)(~key) << 32;
+  first = list_upper(L, lo, hi, v - 1u);
+  last = list_upper(L, first, hi, v | 0xffffffffull) - 1;
+}
+
+struct ListHit {
+  int pos;       // the entry found (-1: the range holds no entry)
+  double excl;   // cumulative mass before it
+  double w;      // its weight
+  double total;  // cumulative mass at the end of the range
+};
+
+// Scan of a sorted range [r0, r1) of L from cumulative `base`: the first entry whose
+// inclusive cumulative exceeds target, or, if none does, the last entry with mass. Thread t
+// owns entries 4t .. 4t+3 of each tile of 4 NT; the sums run in a fixed order.
+__device__ __forceinline__ ListHit list_search(Smem& s, const uint64_t* L, int r0, int r1, float m, double base,
+                                               double target) {
+  int found = INT32_MAX, last = -1;
+  double f_excl = 0.0, f_w = 0.0, l_excl = 0.0, l_w = 0.0;
+  double carry = base;
+  for (int t0 = r0; t0 < r1; t0 += 4 * NT) {
+    const int i0 = t0 + 4 * (int)threadIdx.x;
+    float wf[4];
+    double tt = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wf[i] = (i0 + i < r1) ? wexp(float_of_ord32(key_of(L[i0 + i])), m) : 0.0f;
+      tt += (double)wf[i];
+    }
+    const double wi = wscan_f64(tt);
+    if (lane_id() == 63) s.red_d[wave_id()] = wi;
+    __syncthreads();
+    double run = carry, next = carry;
+#pragma unroll
+    for (int k = 0; k < NWAVE; ++k) {
+      const double r = s.red_d[k];
+      if (k < wave_id()) run += r;
+      next += r;
+    }
+    run += wi - tt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const double w = (double)wf[i];
+      if (w > 0.0) {
+        if (found == INT32_MAX && run + w > target) {
+          found = i0 + i;
+          f_excl = run;
+          f_w = w;
+        }
+        last = i0 + i;
+        l_excl = run;
+        l_w = w;
+      }
+      run += w;
+    }
+    carry = next;
+    __syncthreads();
+  }
+  const int fmin = wmin_i32(found);
+  const uint32_t lmax = wmax_u32((uint32_t)(last + 1));
+  if (lane_id() == 0) {
+    s.red_i[wave_id()] = fmin;
+    s.red_i[NWAVE + wave_id()] = (int)lmax;
+  }
+  __syncthreads();
+  int best = INT32_MAX;
+  uint32_t lbest = 0u;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    best = min(best, s.red_i[w]);
+    lbest = max(lbest, (uint32_t)s.red_i[NWAVE + w]);
+  }
+  ListHit h;
+  h.total = carry;
+  __syncthreads();  // red_i read by every thread before red_d is written below
+  if (best != INT32_MAX) {
+    if (found == best) {
+      s.red_d[0] = f_excl;
+      s.red_d[1] = f_w;
+    }
+    h.pos = best;
+  } else if (lbest > 0u) {
+    if (last + 1 == (int)lbest) {
+      s.red_d[0] = l_excl;
+      s.red_d[1] = l_w;
+    }
+    h.pos = (int)lbest - 1;
+  } else {
+    // no entry with mass: the last entry, weightless
+    if (threadIdx.x == 0) {
+      s.red_d[0] = carry;
+      s.red_d[1] = 0.0;
+    }
+    h.pos = r1 > r0 ? r1 - 1 : -1;
+  }
+  __syncthreads();
+  h.excl = s.red_d[0];
+  h.w = s.red_d[1];
+  __syncthreads();
+  return h;
+}
+
+// Returns false, with m set, when the row must take the bisection path (a counter wrapped
+// or a window holds too many elements). `src0` streams the row once (it may keep it in
+// registers); the later passes read `src`.
+template <int DT, class Src0, class Src>
+__device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0, const Src& src, int b,
+                                             const Divider& dv, int kk, float p, float u, float& m_out) {
+  const int V = a.vocab;
+  const int l = lane_id(), wv = wave_id();
+  uint64_t* const big = (uint64_t*)s.hist;  // the list, once the histogram is no longer read
+
+  // stream: histogram, row maximum, NaN, and sum_i exp(x_i - xmax) with the thread's
+  // running maximum xmax (rescaled once per 16-byte vector)
+  hist_clear(s);
+  lds_barrier();
+  float xmax = -INFINITY;
+  double zs = 0.0;
+  int nan = 0;
+  src0.stream([&](int, const u4& q, int base, bool vvalid) {
+    float xs[4];
+    float cm = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool ok = elem_valid(src0, vvalid, base + e);
+      const float x = x_at<DT>(dv, q, e);
+      if (ok) hist_add_one(s, bin_raw32(x));
+      xs[e] = ok ? x : -INFINITY;
+      nan |= (xs[e] != xs[e]) ? 1 : 0;
+      cm = fmaxf(cm, xs[e]);
+    }
+    const float mn = fmaxf(xmax, cm);
+    const float mr = (mn > -INFINITY) ? mn : 0.0f;
+    float part = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part += __builtin_amdgcn_exp2f((xs[e] - mr) * LOG2E_F);
+    zs = fma(zs, (double)__builtin_amdgcn_exp2f((xmax - mr) * LOG2E_F), (double)part);
+    xmax = mn;
+  });
+  const float m = block_max_nan(xmax, nan, s);  // its barriers also complete the histogram
+  m_out = m;
+  if (m != m || !(m > -INFINITY && m < INFINITY)) {
+    if (threadIdx.x == 0) write_error(a, b, m != m ? PBS_ROW_NAN : PBS_ROW_NONFINITE, m);
+    return true;
+  }
+  {
+    const double zt = (xmax > -INFINITY) ? zs * (double)__builtin_amdgcn_exp2f((xmax - m) * LOG2E_F) : 0.0;
+    const double zw = wsum_f64(zt);
+    if (l == 0) s.red_d2[wv] = zw;
+  }
+  hist_group_counts<DT>(s);
+  __syncthreads();
+  double z_all = 0.0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) z_all += s.red_d2[w];
+  {
+    uint32_t c = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c += s.gcount[4 * l + i];
+    if (wsum_u32(c) != (uint32_t)V) return false;  // a u16 counter wrapped
+  }
+
+  // lower (gmass) and upper (gmass_hi) bounds of the group masses: the non-empty groups
+  // dealt round-robin to the waves, lane l bounding bins 4l .. 4l+3 of the group
+  {
+    uint32_t ne = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ne |= (s.gcount[4 * l + i] != 0u ? 1u : 0u) << i;
+    if (wv == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (!((ne >> i) & 1u)) {
+          s.gmass[4 * l + i] = 0.0;
+          s.gmass_hi[4 * l + i] = 0.0;
+        }
+      }
+    }
+    const uint32_t cnt = (uint32_t)__popc(ne);
+    const uint32_t incl = wscan_u32(cnt);
+    const uint32_t excl = incl - cnt;
+    const uint32_t total = bcast_u32(incl, 63);
+#pragma unroll 1
+    for (uint32_t r = (uint32_t)wv; r < total; r += NWAVE) {
+      const bool mine = r >= excl && r < incl;
+      const int L = first_lane(ballot(mine));
+      uint32_t bits = ne;
+      for (uint32_t k = mine ? r - excl : 0u; k > 0u; --k) bits &= bits - 1u;
+      const uint32_t g = bcast_u32(4u * (uint32_t)l + (uint32_t)(__ffs(bits) - 1), L);
+      uint32_t n4[4];
+      counts4(s, g * 256u + 4u * (uint32_t)l, n4);
+      double plo = 0.0, phi = 0.0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float wl, wh;
+        bin_bounds(g * 256u + 4u * (uint32_t)l + (uint32_t)k, m, wl, wh);
+        plo += (double)n4[k] * (double)wl;
+        phi += (double)n4[k] * (double)wh;
+      }
+      plo = wsum_f64(plo);
+      phi = wsum_f64(phi);
+      if (l == 0) {
+        s.gmass[g] = plo;
+        s.gmass_hi[g] = phi;
+      }
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {
+    // top-down exclusive prefixes: lane l holds groups 255-4l .. 252-4l
+    uint32_t c[4];
+    double w0[4], w1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[i] = s.gcount[255 - 4 * l - i];
+      w0[i] = s.gmass[255 - 4 * l - i];
+      w1[i] = s.gmass_hi[255 - 4 * l - i];
+    }
+    const uint32_t ct = c[0] + c[1] + c[2] + c[3];
+    const double t0 = ((w0[0] + w0[1]) + w0[2]) + w0[3];
+    const double t1 = ((w1[0] + w1[1]) + w1[2]) + w1[3];
+    uint32_t rc = wscan_u32(ct) - ct;
+    double r0 = wscan_f64(t0) - t0, r1 = wscan_f64(t1) - t1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s.gabove_cnt[255 - 4 * l - i] = rc;
+      s.gabove_mass[255 - 4 * l - i] = r0;
+      s.gabove_hi[255 - 4 * l - i] = r1;
+      rc += c[i];
+      r0 += w0[i];
+      r1 += w1[i];
+    }
+  }
+  __syncthreads();
+
+  RowState st = {};
+  st.m = m;
+  st.x_kth = -INFINITY;
+
+  // top-k (sampling.py:15-17): K = the elements with key >= kmin, whose lowest bin is klo
+  const bool topk = kk > 0 && kk < V;
+  uint32_t kmin = 0u, klo = 0u, nk = (uint32_t)V;
+  double zk = z_all;
+  int kties = 0;  // elements of K tied at its lowest value (top-k rows)
+  if (topk) {
+    const int g = find_group_count(s, (uint32_t)kk);
+    uint32_t o, c, ca;
+    bins_count(s, (uint32_t)g, (uint32_t)kk - s.gabove_cnt[g], o, c, ca);
+    const uint32_t cnt_above = s.gabove_cnt[g] + ca;  // elements in bins above the k-th's
+    klo = o;
+    if (cnt_above + c <= SMALLK_CAP) {
+      // everything from the k-th element's bin up fits in one list: the whole row resolves
+      // from it (two passes over the row in all)
+      const Gathered gt = gather_bins<DT>(src, s, big, LIST_CAP, dv, m, 0u, o, 0xffffu, 1u, 0u);
+      if (gt.n != cnt_above + c) return false;  // cannot happen: the counts are exact
+      sort_list(big, gt.n);
+      kmin = key_of(big[kk - 1]);
+      int f0, f1;
+      list_key_range(big, 0, (int)gt.n, kmin, f0, f1);
+      st.x_kth = float_of_ord32(kmin);
+      st.kord_lo = kmin;
+      const int nK = f1 + 1;
+      const ListHit hz = list_search(s, big, 0, nK, m, 0.0, INFINITY);
+      zk = hz.total;
+      st.zk = zk;
+      int nkeep = nK;
+      if (p < 1.0f) {
+        const ListHit hc = list_search(s, big, 0, nK, m, 0.0, (double)p * zk);
+        const uint32_t ckey = key_of(big[hc.pos]);
+        int c0, c1;
+        list_key_range(big, 0, nK, ckey, c0, c1);
+        st.x_cut = float_of_ord32(ckey);
+        st.n_cut_tie = c1 - c0 + 1;
+        st.n_cut_keep = hc.pos - c0 + 1;
+        st.zp = hc.excl + hc.w;
+        nkeep = hc.pos + 1;
+      } else {
+        st.x_cut = st.x_kth;
+        st.n_cut_tie = st.n_cut_keep = f1 - f0 + 1;
+        st.zp = zk;
+      }
+      st.n_kept = nkeep;
+      // the draw (sampling.py:26-27, inverse-CDF form)
+      st.target = (double)u * st.zp;
+      const ListHit hd = list_search(s, big, 0, nkeep, m, 0.0, st.target);
+      if (threadIdx.x == 0) write_info(a, b, index_of(big[hd.pos]), PBS_ROW_OK, st);
+      return true;
+    }
+    // the k-th element's bin alone, and the exact mass above it
+    const Gathered gt = gather_bins<DT>(src, s, s.list, GATHER_CAP, dv, m, 0u, o, o, 1u, 0u);
+    if (gt.n != c || gt.n > GATHER_CAP) return false;
+    sort_list(s.list, gt.n);
+    kmin = key_of(s.list[kk - 1 - (int)cnt_above]);
+    int f0, f1;
+    list_key_range(s.list, 0, (int)gt.n, kmin, f0, f1);
+    st.x_kth = float_of_ord32(kmin);
+    const ListHit hz = list_search(s, s.list, 0, f1 + 1, m, gt.above1, INFINITY);
+    zk = hz.total;
+    nk = cnt_above + (uint32_t)f1 + 1u;
+    kties = f1 - f0 + 1;
+  }
+  st.kord_lo = kmin;
+  st.zk = zk;
+
+  // Windows. The cutoff (top-p, sampling.py:18-25) is the first element of K whose
+  // inclusive mass exceeds tau = p Z_K; it lies in bins [c_lo, c_hi]. Z_P, its inclusive
+  // mass, lies in (tau, tau + its weight], which bounds the draw's target u Z_P; the draw
+  // lies in bins [d_lo, d_hi], at or above c_hi.
+  const bool cut = p < 1.0f;
+  const double tau = (double)p * zk;
+  uint32_t c_lo = 1u, c_hi = 0u;
+  double t_lo, t_hi;
+  if (cut) {
+    const uint32_t ob = find_bin_bound<true>(s, klo, tau, m);
+    const uint32_t oa = find_bin_bound<false>(s, klo, tau, m);
+    c_lo = min(oa, ob);
+    c_hi = max(oa, ob);
+    float wl, wh;
+    bin_bounds(c_hi, m, wl, wh);
+    t_lo = (double)u * tau * (1.0 - 1e-6);
+    t_hi = (double)u * (tau + (double)wh) * (1.0 + 1e-6);
+  } else {
+    t_lo = (double)u * zk * (1.0 - 1e-6);
+    t_hi = (double)u * zk * (1.0 + 1e-6);
+  }
+  const uint32_t d_hi = find_bin_bound<true>(s, klo, t_lo, m);
+  const uint32_t d_lo = find_bin_bound<false>(s, klo, t_hi, m);
+  // window 1 holds the draw's bins (and the cutoff's when they meet); window 2 the cutoff's
+  uint32_t lo1 = d_lo, hi1 = d_hi, lo2 = 1u, hi2 = 0u;
+  if (cut) {
+    if (d_lo <= c_hi + 1u) {
+      lo1 = min(d_lo, c_lo);
+      hi1 = max(d_hi, c_hi);
+    } else {
+      lo2 = c_lo;
+      hi2 = c_hi;
+    }
+  }
+  const bool split = lo2 <= hi2;
+  // elements above the list's cutoff segment (all in K: the windows lie at or above klo)
+  const uint32_t n_above_seg = cut ? count_bins_ge(s, (split ? hi2 : hi1) + 1u) : 0u;
+  const uint32_t n_neg_inf = hist_count(s, ord32(-INFINITY) >> 16);
+  const Gathered gw = gather_bins<DT>(src, s, big, LIST_CAP, dv, m, kmin, lo1, hi1, lo2, hi2);
+  if (gw.n > LIST_CAP) return false;
+  sort_list(big, gw.n);
+  const int n = (int)gw.n, n1 = (int)gw.n1;
+  const int cs0 = split ? n1 : 0;  // the cutoff's segment of the list and the mass above it
+  const double cbase = split ? gw.above2 : gw.above1;
+  int dend = n;                     // the draw searches [0, dend) of window 1 ...
+  int cpos = n - 1;
+  if (cut) {
+    const ListHit hc = list_search(s, big, cs0, n, m, cbase, tau);
+    if (hc.pos < 0) return false;
+    const uint32_t ckey = key_of(big[hc.pos]);
+    int c0, c1;
+    list_key_range(big, cs0, n, ckey, c0, c1);
+    st.x_cut = float_of_ord32(ckey);
+    st.n_cut_tie = c1 - c0 + 1;
+    st.n_cut_keep = hc.pos - c0 + 1;
+    st.zp = hc.excl + hc.w;
+    st.n_kept = (int)n_above_seg + (hc.pos - cs0) + 1;
+    cpos = hc.pos;
+    dend = split ? n1 : hc.pos + 1;
+  } else {
+    st.zp = zk;
+    st.n_kept = (int)nk;
+    if (topk) {
+      st.x_cut = st.x_kth;
+      st.n_cut_tie = st.n_cut_keep = kties;
+    } else {
+      // every element is kept: the lowest "cutoff" value is -inf, with all its ties
+      st.x_cut = -INFINITY;
+      st.n_cut_tie = st.n_cut_keep = (int)n_neg_inf;
+    }
+  }
+  // the draw (sampling.py:26-27, inverse-CDF form): in window 1, or in the cutoff's
+  // segment, up to the cutoff, when the target lies at or past the mass above it
+  const double t = (double)u * st.zp;
+  st.target = t;
+  const ListHit hd = (split && t >= gw.above2) ? list_search(s, big, n1, cpos + 1, m, gw.above2, t)
+                                               : list_search(s, big, 0, dend, m, gw.above1, t);
+  if (hd.pos < 0) return false;
+  if (threadIdx.x == 0) write_info(a, b, index_of(big[hd.pos]), PBS_ROW_OK, st);
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------
 // one row
 // ---------------------------------------------------------------------------------------
 template <int DT, class Src>
@@ -1708,9 +2321,10 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
   Divider dv;
   dv.init(T);
   if constexpr (Src::kVector) {
-    // The bisection passes re-read the row, so no register copy of it stays live across
-    // them. 16-bit rows get here only when a histogram counter wrapped (one value more
-    // than 65535 times); their first pass re-reads the row as well.
+    // Passes after the first re-read the row (from cache when it was just read), so no
+    // register copy of it stays live across them. 16-bit rows get here only when a
+    // histogram counter wrapped (one value more than 65535 times); their first pass
+    // re-reads the row as well.
     MemRow<DT> mem;
     mem.init((const uint8_t*)a.logits + (size_t)lrow * (size_t)a.row_stride * elt, a.nvec, a.vocab);
     float m;
@@ -1718,14 +2332,17 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
       if (sample_row16<DT>(a, s, src, b, T, kk, p, u)) return;
       m = bis_max<DT>(mem, s, dv, false);
     } else {
-      m = bis_max<DT>(src, s, dv, true);
+      if (sample_row32<DT>(a, s, src, mem, b, dv, kk, p, u, m)) return;
     }
     sample_row_bisect<DT>(a, s, mem, b, m, dv, kk, p, u);
   } else {
+    float m;
     if constexpr (B16) {
       if (sample_row16<DT>(a, s, src, b, T, kk, p, u)) return;
+      m = bis_max<DT>(src, s, dv, false);
+    } else {
+      if (sample_row32<DT>(a, s, src, src, b, dv, kk, p, u, m)) return;
     }
-    const float m = bis_max<DT>(src, s, dv, !B16);
     sample_row_bisect<DT>(a, s, src, b, m, dv, kk, p, u);
   }
 }
