@@ -37,7 +37,7 @@ constexpr int NWAVE = NT / 64;     // wave64
 constexpr int HIST_WORDS = 32768;  // 64K packed u16 counters = 128 KB of LDS
 constexpr int NGROUP = 256;        // histogram groups of 256 ords (high byte of a 16-bit ord)
 constexpr int PIPE = 4;            // 16-byte loads per thread in flight while a row streams in
-constexpr int GATHER_CAP = 2048;   // fp32 rows: elements one search window may gather into LDS
+constexpr int NBUCKET = 256;       // fp32 rows: buckets per level of a list search
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -330,6 +330,11 @@ struct Divider {
   }
 };
 
+// T == 1: the quotient is the value itself
+struct UnitDivider {
+  __device__ __forceinline__ float operator()(float a) const { return a; }
+};
+
 // ---------------------------------------------------------------------------------------
 // kernel arguments and per-row shared state
 // ---------------------------------------------------------------------------------------
@@ -376,12 +381,17 @@ struct __align__(16) Smem {
   double gabove_mass[NGROUP];    // mass strictly above the group
   union {
     double subabove[NGROUP * 8];  // 16-bit rows: mass of the subgroups (32 ords) above each one, in its group
-    uint64_t list[GATHER_CAP];    // fp32 rows: gathered (~key << 32 | index) of one search window
+    struct {                      // fp32 rows
+      double gmass_hi[NGROUP];    // upper bounds of the group masses (gmass holds the lower bounds)
+      double gabove_hi[NGROUP];   // upper bound of the mass above each group
+      uint64_t bmass[NBUCKET];    // list searches: fixed-point mass per bucket
+      uint32_t bcnt[NBUCKET];     //   and entries per bucket
+    } f32;
   };
-  double gmass_hi[NGROUP];       // fp32 rows: upper bounds of the group masses (gmass holds lower bounds)
-  double gabove_hi[NGROUP];
   uint32_t list_n;               // fp32 rows: entries gathered
-  uint32_t list_hit;             // fp32 rows: result of a list search
+  uint64_t pick;                 // fp32 rows: the entry a list search found
+  uint32_t cand[NWAVE], cand_cnt[NWAVE], last[NWAVE], last_cnt[NWAVE];  // list searches, per wave
+  double cand_excl[NWAVE], last_excl[NWAVE];
   double red_d[NWAVE];
   double red_d2[NWAVE];
   float red_f[NWAVE];
@@ -1489,8 +1499,8 @@ __device__ __forceinline__ float weight32(float x, float m) {
   return ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
 }
 
-template <int DT>
-__device__ __forceinline__ float x_at(const Divider& dv, const u4& q, int e) {
+template <int DT, class Div>
+__device__ __forceinline__ float x_at(const Div& dv, const u4& q, int e) {
   return dv(raw_to_float<DT>(elem_raw<DT>(q, e)));
 }
 
@@ -1676,19 +1686,27 @@ __device__ __forceinline__ void sample_row_bisect(const KArgs& a, Smem& s, const
 // cumulative from the top: a search by count lands on one bin; a search by mass lands
 // between the bin where the upper bounds cross the target (the cumulative can cross no
 // earlier) and the bin where the lower bounds do (no later). One more pass gathers those
-// windows' elements into LDS as (~key << 32 | index) and sums the exact mass above each
-// window; sorted ascending (key descending, index ascending), the windows are scanned
-// exactly. Top-k rows whose k-th element lies in the top few thousand gather everything
-// from its bin up and resolve the row from that one list. Rows whose windows hold more
-// elements than LDS takes, or whose counters wrap, take the bisection path.
+// windows' elements into LDS as entries E = (~key << 32 | index), whose ascending order is
+// the sampling order (value descending, index ascending), and sums the exact mass above
+// each window. Searches in the gathered list narrow an interval of E over 256 buckets per
+// level; weights enter the bucket sums as fixed-point integers, so every sum is exact and
+// independent of the gather's order. Top-k rows whose k-th element lies within the top few
+// thousand gather everything from its bin up instead and resolve from that list alone.
+// Rows whose windows hold more elements than LDS takes, or whose counters wrap, take the
+// bisection path.
 // ---------------------------------------------------------------------------------------
-constexpr uint32_t LIST_CAP = HIST_WORDS / 2;  // entries of the list that reuses the histogram
+constexpr uint32_t LIST_CAP = HIST_WORDS / 2;  // entries of the list, which reuses the histogram
 constexpr uint32_t SMALLK_CAP = 4096;          // top-k rows resolved from one list up to this size
 constexpr float LOG2E_F = 1.44269504088896341f;
+constexpr double FIXQ = 0x1p-38;               // fixed-point weight unit
 
 // exp(x - m) as the fp32 searches compute it: fp32 difference and product, hardware exp2
 __device__ __forceinline__ float wexp(float x, float m) {
   return (x > -INFINITY) ? __builtin_amdgcn_exp2f((x - m) * LOG2E_F) : 0.0f;
+}
+// floor(w * 2^38) for 0 <= w < 2: at most 2^39, so 2^14 of them sum exactly in a double
+__device__ __forceinline__ uint64_t fixq(float w) {
+  return (uint64_t)((double)w * 0x1p38);
 }
 // histogram index of x: the top 16 bits of its pattern, -0 folded onto +0 (the raw whose
 // unfolded ord is ord32(x) >> 16)
@@ -1696,8 +1714,16 @@ __device__ __forceinline__ uint32_t bin_raw32(float x) {
   const uint32_t b = __float_as_uint(x);
   return (b == 0x80000000u) ? 0u : (b >> 16);
 }
+// (HIP's min/max on mixed 64-bit integer types resolve to the double overloads: these do not)
+__device__ __forceinline__ uint64_t min_u64(uint64_t a, uint64_t b) { return a < b ? a : b; }
 __device__ __forceinline__ uint32_t key_of(uint64_t e) { return ~(uint32_t)(e >> 32); }
 __device__ __forceinline__ int index_of(uint64_t e) { return (int)(uint32_t)e; }
+__device__ __forceinline__ float value_of(uint64_t e) { return float_of_ord32(key_of(e)); }
+// the interval of E holding key k, and the one holding bins [lo, hi]
+__device__ __forceinline__ uint64_t e_first(uint32_t key) { return (uint64_t)(~key) << 32; }
+__device__ __forceinline__ uint64_t e_last(uint32_t key) { return ((uint64_t)(~key) << 32) | 0xffffffffull; }
+__device__ __forceinline__ uint64_t e_bins_first(uint32_t hi) { return e_first((hi << 16) | 0xffffu); }
+__device__ __forceinline__ uint64_t e_bins_last(uint32_t lo) { return e_last(lo << 16); }
 
 // Bounds on wexp(x, m) over the x of bin o that a row with maximum m can hold. wexp is
 // monotone up to its last-ulp rounding; the factors cover that and the fp32 partial sums
@@ -1716,12 +1742,32 @@ __device__ __forceinline__ uint32_t count_bins_ge(const Smem& s, uint32_t t) {
   return count_above_in_group(s, g, t - 1u) + s.gabove_cnt[g];
 }
 
+// lower (HI = false) or upper bound of the mass in bins > o (whole wave)
+template <bool HI>
+__device__ __forceinline__ double bound_above(const Smem& s, uint32_t o, float m) {
+  const uint32_t g = o >> 8;
+  const int l = lane_id();
+  uint32_t n4[4];
+  counts4(s, g * 256u + 4u * (uint32_t)l, n4);
+  double w = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t b = g * 256u + 4u * (uint32_t)l + (uint32_t)i;
+    if (b > o && n4[i]) {
+      float wl, wh;
+      bin_bounds(b, m, wl, wh);
+      w += (double)n4[i] * (double)(HI ? wh : wl);
+    }
+  }
+  return wsum_f64(w) + (HI ? s.f32.gabove_hi[g] : s.gabove_mass[g]);
+}
+
 // The bin >= lo (descending from the top) where the cumulative bound mass, upper bounds
 // (HI) or lower bounds, first exceeds target; the lowest non-empty bin >= lo if it never
 // does. Whole wave, no barrier.
 template <bool HI>
 __device__ __forceinline__ uint32_t find_bin_bound(const Smem& s, uint32_t lo, double target, float m) {
-  const double* above = HI ? s.gabove_hi : s.gabove_mass;
+  const double* above = HI ? s.f32.gabove_hi : s.gabove_mass;
   const int l = lane_id();
   const uint32_t glo = lo >> 8;
   // the lowest non-empty group >= glo whose mass starts at or before target
@@ -1782,210 +1828,220 @@ __device__ __forceinline__ uint32_t find_bin_bound(const Smem& s, uint32_t lo, d
   return g * 256u + 255u - 4u * (uint32_t)L - bcast_u32((uint32_t)fi, L);
 }
 
-struct Gathered {
-  uint32_t n;     // matches (more than the list's capacity: the list holds only some)
-  uint32_t n1;    // matches in the first window
-  double above1;  // exact mass of the elements (key >= kmin) in bins above hi1
-  double above2;  // ... above hi2
-};
-
-// One pass over the row: every element with key >= kmin whose bin lies in [lo1, hi1] or
-// [lo2, hi2] (either may be empty: lo > hi) goes into L, unsorted.
-template <int DT, class Src>
-__device__ __forceinline__ Gathered gather_bins(const Src& src, Smem& s, uint64_t* L, uint32_t cap,
-                                                const Divider& dv, float m, uint32_t kmin, uint32_t lo1,
-                                                uint32_t hi1, uint32_t lo2, uint32_t hi2) {
+// One pass over the row: every element whose bin lies in one of the NW windows [lo_i,
+// hi_i] (they may overlap) goes into L, unsorted; above_i gets the exact mass of the
+// elements in bins above window i. Returns the number of entries (more than LIST_CAP: the
+// list holds only some).
+template <int DT, int NW, class Src, class Div>
+__device__ __forceinline__ uint32_t gather_bins(const Src& src, Smem& s, uint64_t* L, const Div& dv, float m,
+                                                uint32_t lo0, uint32_t hi0, uint32_t lo1, uint32_t hi1,
+                                                uint32_t lo2, uint32_t hi2, double& above0, double& above1,
+                                                double& above2) {
+  const uint32_t lo[3] = {lo0, lo1, lo2}, hi[3] = {hi0, hi1, hi2};
   if (threadIdx.x == 0) s.list_n = 0u;
   __syncthreads();
-  double acc1 = 0.0, acc2 = 0.0;
-  uint32_t c1 = 0u;
+  double acc[NW];
+#pragma unroll
+  for (int r = 0; r < NW; ++r) acc[r] = 0.0;
   src.for_each([&](int, const u4& q, int base, bool vvalid) {
-    float p1 = 0.0f, p2 = 0.0f;
+    float part[NW];
+#pragma unroll
+    for (int r = 0; r < NW; ++r) part[r] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float x = x_at<DT>(dv, q, e);
       const uint32_t key = ord32(x);
       const uint32_t o = key >> 16;
-      const bool in = elem_valid(src, vvalid, base + e) && key >= kmin;
-      const float w = wexp(x, m);
-      p1 += (in && o > hi1) ? w : 0.0f;
-      p2 += (in && o > hi2) ? w : 0.0f;
-      const bool w1 = o >= lo1 && o <= hi1;
-      if (in && (w1 || (o >= lo2 && o <= hi2))) {
+      const bool ok = elem_valid(src, vvalid, base + e);
+      const float w = ok ? wexp(x, m) : 0.0f;
+      bool in = false;
+#pragma unroll
+      for (int r = 0; r < NW; ++r) {
+        part[r] += (o > hi[r]) ? w : 0.0f;
+        in = in || (o - lo[r] <= hi[r] - lo[r]);
+      }
+      if (ok && in) {
         const uint32_t slot = atomicAdd(&s.list_n, 1u);
-        if (slot < cap) L[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
-        c1 += w1 ? 1u : 0u;
+        if (slot < LIST_CAP) L[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
       }
     }
-    acc1 += (double)p1;
-    acc2 += (double)p2;
+#pragma unroll
+    for (int r = 0; r < NW; ++r) acc[r] += (double)part[r];
   });
-  acc1 = wsum_f64(acc1);
-  acc2 = wsum_f64(acc2);
-  c1 = wsum_u32(c1);
+  double tot[3] = {0.0, 0.0, 0.0};
+#pragma unroll
+  for (int r = 0; r < NW; ++r) {
+    const double a = wsum_f64(acc[r]);
+    if (lane_id() == 0) s.red_d[wave_id()] = a;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) tot[r] += s.red_d[w];
+    __syncthreads();
+  }
+  above0 = tot[0];
+  above1 = tot[1];
+  above2 = tot[2];
+  const uint32_t n = s.list_n;
+  __syncthreads();
+  return n;
+}
+
+// count and fixed-point mass (FIXQ units, exact) of the entries of L[0, n) in [ea, eb]
+template <bool MASS>
+__device__ __forceinline__ void list_sum(Smem& s, const uint64_t* L, int n, uint64_t ea, uint64_t eb, float m,
+                                         uint32_t& cnt, double& mass) {
+  uint32_t c = 0u;
+  uint64_t q = 0u;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const uint64_t e = L[i];
+    if (e >= ea && e <= eb) {
+      ++c;
+      if (MASS) q += fixq(wexp(value_of(e), m));
+    }
+  }
+  c = wsum_u32(c);
+  const double qd = MASS ? wsum_f64((double)q) : 0.0;
   if (lane_id() == 0) {
-    s.red_d[wave_id()] = acc1;
-    s.red_d2[wave_id()] = acc2;
-    s.red_i[wave_id()] = (int)c1;
+    s.red_i[wave_id()] = (int)c;
+    s.red_d[wave_id()] = qd;
   }
   __syncthreads();
-  Gathered r;
-  r.n = s.list_n;
-  r.above1 = 0.0;
-  r.above2 = 0.0;
-  r.n1 = 0u;
+  cnt = 0u;
+  mass = 0.0;
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) {
-    r.above1 += s.red_d[w];
-    r.above2 += s.red_d2[w];
-    r.n1 += (uint32_t)s.red_i[w];
+    cnt += (uint32_t)s.red_i[w];
+    mass += s.red_d[w];
   }
   __syncthreads();
-  return r;
 }
 
-// Bitonic sort of L[0, n) ascending (n <= the list's power-of-two capacity), padded with
-// ~0 up to the next power of two. Entries are distinct: the order is unique.
-__device__ __forceinline__ void sort_list(uint64_t* L, uint32_t n) {
-  uint32_t np = 2u;
-  while (np < n) np <<= 1;
-  for (uint32_t i = n + threadIdx.x; i < np; i += NT) L[i] = ~0ull;
-  __syncthreads();
-  for (uint32_t k = 2u; k <= np; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
-      for (uint32_t t = threadIdx.x; t < (np >> 1); t += NT) {
-        const uint32_t i = ((t & ~(j - 1u)) << 1) | (t & (j - 1u));
-        const uint64_t a = L[i], b = L[i | j];
-        if ((a > b) == ((i & k) == 0u)) {
-          L[i] = b;
-          L[i | j] = a;
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
-
-// first position in [lo, hi) of a sorted list whose entry exceeds v (every thread)
-__device__ __forceinline__ int list_upper(const uint64_t* L, int lo, int hi, uint64_t v) {
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (L[mid] > v) hi = mid;
-    else lo = mid + 1;
-  }
-  return lo;
-}
-// positions [first, last] of the entries with key `key` in [lo, hi)
-__device__ __forceinline__ void list_key_range(const uint64_t* L, int lo, int hi, uint32_t key, int& first,
-                                               int& last) {
-  const uint64_t v = (uint64_t)(~key) << 32;
-  first = list_upper(L, lo, hi, v - 1u);
-  last = list_upper(L, first, hi, v | 0xffffffffull) - 1;
-}
-
-struct ListHit {
-  int pos;       // the entry found (-1: the range holds no entry)
-  double excl;   // cumulative mass before it
-  double w;      // its weight
-  double total;  // cumulative mass at the end of the range
+struct Pick {
+  uint64_t e;   // the entry (~0: the interval held none)
+  double excl;  // cumulative before it
+  double w;     // its weight (fixed-point, as the cumulative counts it)
 };
 
-// Scan of a sorted range [r0, r1) of L from cumulative `base`: the first entry whose
-// inclusive cumulative exceeds target, or, if none does, the last entry with mass. Thread t
-// owns entries 4t .. 4t+3 of each tile of 4 NT; the sums run in a fixed order.
-__device__ __forceinline__ ListHit list_search(Smem& s, const uint64_t* L, int r0, int r1, float m, double base,
-                                               double target) {
-  int found = INT32_MAX, last = -1;
-  double f_excl = 0.0, f_w = 0.0, l_excl = 0.0, l_w = 0.0;
-  double carry = base;
-  for (int t0 = r0; t0 < r1; t0 += 4 * NT) {
-    const int i0 = t0 + 4 * (int)threadIdx.x;
-    float wf[4];
-    double tt = 0.0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      wf[i] = (i0 + i < r1) ? wexp(float_of_ord32(key_of(L[i0 + i])), m) : 0.0f;
-      tt += (double)wf[i];
+// The first entry of L[0, n) in [ea, eb], in ascending order, whose inclusive cumulative
+// from `base` exceeds target: weights are the entries' fixed-point masses (MASS) or 1 (a
+// count). If none does, the last entry with weight. Each level spreads the interval over
+// NBUCKET buckets, sums them exactly and keeps the bucket where the cumulative crosses,
+// until one entry is left.
+template <bool MASS>
+__device__ __forceinline__ Pick list_pick(Smem& s, const uint64_t* L, int n, uint64_t ea, uint64_t eb, float m,
+                                          double base, double target) {
+  const int t = threadIdx.x, l = lane_id(), wv = wave_id();
+  const double unit = MASS ? FIXQ : 1.0;
+  uint64_t lo = ea, hi = eb;
+  double B = base;
+  uint32_t cnt = 0u;
+#pragma unroll 1
+  for (int level = 0; level < 8; ++level) {
+    const uint64_t span = hi - lo;
+    const int sh = (span >> 8) ? 64 - __clzll((unsigned long long)(span >> 8)) : 0;
+    if (t < NBUCKET) {
+      s.f32.bmass[t] = 0u;
+      s.f32.bcnt[t] = 0u;
     }
-    const double wi = wscan_f64(tt);
-    if (lane_id() == 63) s.red_d[wave_id()] = wi;
     __syncthreads();
-    double run = carry, next = carry;
-#pragma unroll
-    for (int k = 0; k < NWAVE; ++k) {
-      const double r = s.red_d[k];
-      if (k < wave_id()) run += r;
-      next += r;
-    }
-    run += wi - tt;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const double w = (double)wf[i];
-      if (w > 0.0) {
-        if (found == INT32_MAX && run + w > target) {
-          found = i0 + i;
-          f_excl = run;
-          f_w = w;
-        }
-        last = i0 + i;
-        l_excl = run;
-        l_w = w;
+    for (int i = t; i < n; i += NT) {
+      const uint64_t e = L[i];
+      if (e >= lo && e <= hi) {
+        const uint32_t bk = (uint32_t)((e - lo) >> sh);
+        atomicAdd(&s.f32.bcnt[bk], 1u);
+        if (MASS) atomicAdd((unsigned long long*)&s.f32.bmass[bk], (unsigned long long)fixq(wexp(value_of(e), m)));
       }
-      run += w;
     }
-    carry = next;
     __syncthreads();
-  }
-  const int fmin = wmin_i32(found);
-  const uint32_t lmax = wmax_u32((uint32_t)(last + 1));
-  if (lane_id() == 0) {
-    s.red_i[wave_id()] = fmin;
-    s.red_i[NWAVE + wave_id()] = (int)lmax;
-  }
-  __syncthreads();
-  int best = INT32_MAX;
-  uint32_t lbest = 0u;
+    // buckets in ascending order: thread t < NBUCKET holds bucket t (waves 0-3)
+    uint32_t c = 0u;
+    double v = 0.0;
+    if (t < NBUCKET) {
+      c = s.f32.bcnt[t];
+      v = MASS ? (double)s.f32.bmass[t] : (double)c;
+    }
+    const double vi = wscan_f64(v);  // integers below 2^53: exact
+    if (l == 63) s.red_d2[wv] = vi;
+    __syncthreads();
+    double before = 0.0;
 #pragma unroll
-  for (int w = 0; w < NWAVE; ++w) {
-    best = min(best, s.red_i[w]);
-    lbest = max(lbest, (uint32_t)s.red_i[NWAVE + w]);
+    for (int k = 0; k < NBUCKET / 64; ++k) before += (k < wv) ? s.red_d2[k] : 0.0;
+    const double excl = before + vi - v;
+    const bool cross = t < NBUCKET && v > 0.0 && B + (excl + v) * unit > target;
+    const uint64_t hc = ballot(cross);
+    const uint64_t hl = ballot(t < NBUCKET && v > 0.0);
+    if (l == 0) {
+      s.cand[wv] = hc ? (uint32_t)(64 * wv + first_lane(hc)) : 0xffffffffu;
+      s.last[wv] = hl ? (uint32_t)(64 * wv + 63 - __clzll((unsigned long long)hl)) : 0xffffffffu;
+    }
+    if (hc && l == first_lane(hc)) {
+      s.cand_excl[wv] = excl;
+      s.cand_cnt[wv] = c;
+    }
+    if (hl && l == 63 - __clzll((unsigned long long)hl)) {
+      s.last_excl[wv] = excl;
+      s.last_cnt[wv] = c;
+    }
+    __syncthreads();
+    uint32_t bk = 0xffffffffu, lb = 0xffffffffu;
+    double bex = 0.0, lex = 0.0;
+    uint32_t bc = 0u, lc = 0u;
+#pragma unroll
+    for (int k = 0; k < NBUCKET / 64; ++k) {
+      const uint32_t ck = s.cand[k];
+      if (ck != 0xffffffffu && bk == 0xffffffffu) {
+        bk = ck;
+        bex = s.cand_excl[k];
+        bc = s.cand_cnt[k];
+      }
+      const uint32_t lk = s.last[k];
+      if (lk != 0xffffffffu) {
+        lb = lk;
+        lex = s.last_excl[k];
+        lc = s.last_cnt[k];
+      }
+    }
+    if (bk == 0xffffffffu) {
+      bk = lb;
+      bex = lex;
+      bc = lc;
+    }
+    if (bk == 0xffffffffu) {
+      // no entry with weight in the interval
+      Pick p;
+      p.e = ~0ull;
+      p.excl = B;
+      p.w = 0.0;
+      return p;
+    }
+    B += bex * unit;
+    cnt = bc;
+    lo += (uint64_t)bk << sh;
+    hi = min_u64(hi, lo + (((uint64_t)1 << sh) - 1u));
+    if (cnt == 1u || sh == 0) break;
   }
-  ListHit h;
-  h.total = carry;
-  __syncthreads();  // red_i read by every thread before red_d is written below
-  if (best != INT32_MAX) {
-    if (found == best) {
-      s.red_d[0] = f_excl;
-      s.red_d[1] = f_w;
-    }
-    h.pos = best;
-  } else if (lbest > 0u) {
-    if (last + 1 == (int)lbest) {
-      s.red_d[0] = l_excl;
-      s.red_d[1] = l_w;
-    }
-    h.pos = (int)lbest - 1;
-  } else {
-    // no entry with mass: the last entry, weightless
-    if (threadIdx.x == 0) {
-      s.red_d[0] = carry;
-      s.red_d[1] = 0.0;
-    }
-    h.pos = r1 > r0 ? r1 - 1 : -1;
+  // the interval now holds one entry (or one value of E)
+  if (t == 0) s.pick = ~0ull;
+  __syncthreads();
+  for (int i = t; i < n; i += NT) {
+    const uint64_t e = L[i];
+    if (e >= lo && e <= hi) s.pick = e;
   }
   __syncthreads();
-  h.excl = s.red_d[0];
-  h.w = s.red_d[1];
+  Pick p;
+  p.e = s.pick;
+  p.excl = B;
+  p.w = MASS ? (double)fixq(wexp(value_of(p.e), m)) * FIXQ : 1.0;
   __syncthreads();
-  return h;
+  return p;
 }
 
 // Returns false, with m set, when the row must take the bisection path (a counter wrapped
 // or a window holds too many elements). `src0` streams the row once (it may keep it in
 // registers); the later passes read `src`.
-template <int DT, class Src0, class Src>
+template <int DT, class Src0, class Src, class Div>
 __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0, const Src& src, int b,
-                                             const Divider& dv, int kk, float p, float u, float& m_out) {
+                                             const Div& dv, int kk, float p, float u, float& m_out) {
   const int V = a.vocab;
   const int l = lane_id(), wv = wave_id();
   uint64_t* const big = (uint64_t*)s.hist;  // the list, once the histogram is no longer read
@@ -2051,7 +2107,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
       for (int i = 0; i < 4; ++i) {
         if (!((ne >> i) & 1u)) {
           s.gmass[4 * l + i] = 0.0;
-          s.gmass_hi[4 * l + i] = 0.0;
+          s.f32.gmass_hi[4 * l + i] = 0.0;
         }
       }
     }
@@ -2080,7 +2136,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
       phi = wsum_f64(phi);
       if (l == 0) {
         s.gmass[g] = plo;
-        s.gmass_hi[g] = phi;
+        s.f32.gmass_hi[g] = phi;
       }
     }
   }
@@ -2093,7 +2149,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     for (int i = 0; i < 4; ++i) {
       c[i] = s.gcount[255 - 4 * l - i];
       w0[i] = s.gmass[255 - 4 * l - i];
-      w1[i] = s.gmass_hi[255 - 4 * l - i];
+      w1[i] = s.f32.gmass_hi[255 - 4 * l - i];
     }
     const uint32_t ct = c[0] + c[1] + c[2] + c[3];
     const double t0 = ((w0[0] + w0[1]) + w0[2]) + w0[3];
@@ -2104,7 +2160,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     for (int i = 0; i < 4; ++i) {
       s.gabove_cnt[255 - 4 * l - i] = rc;
       s.gabove_mass[255 - 4 * l - i] = r0;
-      s.gabove_hi[255 - 4 * l - i] = r1;
+      s.f32.gabove_hi[255 - 4 * l - i] = r1;
       rc += c[i];
       r0 += w0[i];
       r1 += w1[i];
@@ -2115,151 +2171,168 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   RowState st = {};
   st.m = m;
   st.x_kth = -INFINITY;
+  const bool cut = p < 1.0f;
 
-  // top-k (sampling.py:15-17): K = the elements with key >= kmin, whose lowest bin is klo
+  // top-k (sampling.py:15-17): K = the elements with key >= kmin; the k-th lies in bin klo
   const bool topk = kk > 0 && kk < V;
-  uint32_t kmin = 0u, klo = 0u, nk = (uint32_t)V;
-  double zk = z_all;
-  int kties = 0;  // elements of K tied at its lowest value (top-k rows)
+  uint32_t klo = 0u, kc = 0u, kabove = 0u;
   if (topk) {
     const int g = find_group_count(s, (uint32_t)kk);
-    uint32_t o, c, ca;
-    bins_count(s, (uint32_t)g, (uint32_t)kk - s.gabove_cnt[g], o, c, ca);
-    const uint32_t cnt_above = s.gabove_cnt[g] + ca;  // elements in bins above the k-th's
-    klo = o;
-    if (cnt_above + c <= SMALLK_CAP) {
-      // everything from the k-th element's bin up fits in one list: the whole row resolves
-      // from it (two passes over the row in all)
-      const Gathered gt = gather_bins<DT>(src, s, big, LIST_CAP, dv, m, 0u, o, 0xffffu, 1u, 0u);
-      if (gt.n != cnt_above + c) return false;  // cannot happen: the counts are exact
-      sort_list(big, gt.n);
-      kmin = key_of(big[kk - 1]);
-      int f0, f1;
-      list_key_range(big, 0, (int)gt.n, kmin, f0, f1);
-      st.x_kth = float_of_ord32(kmin);
-      st.kord_lo = kmin;
-      const int nK = f1 + 1;
-      const ListHit hz = list_search(s, big, 0, nK, m, 0.0, INFINITY);
-      zk = hz.total;
-      st.zk = zk;
-      int nkeep = nK;
-      if (p < 1.0f) {
-        const ListHit hc = list_search(s, big, 0, nK, m, 0.0, (double)p * zk);
-        const uint32_t ckey = key_of(big[hc.pos]);
-        int c0, c1;
-        list_key_range(big, 0, nK, ckey, c0, c1);
-        st.x_cut = float_of_ord32(ckey);
-        st.n_cut_tie = c1 - c0 + 1;
-        st.n_cut_keep = hc.pos - c0 + 1;
-        st.zp = hc.excl + hc.w;
-        nkeep = hc.pos + 1;
-      } else {
-        st.x_cut = st.x_kth;
-        st.n_cut_tie = st.n_cut_keep = f1 - f0 + 1;
-        st.zp = zk;
-      }
-      st.n_kept = nkeep;
-      // the draw (sampling.py:26-27, inverse-CDF form)
-      st.target = (double)u * st.zp;
-      const ListHit hd = list_search(s, big, 0, nkeep, m, 0.0, st.target);
-      if (threadIdx.x == 0) write_info(a, b, index_of(big[hd.pos]), PBS_ROW_OK, st);
-      return true;
-    }
-    // the k-th element's bin alone, and the exact mass above it
-    const Gathered gt = gather_bins<DT>(src, s, s.list, GATHER_CAP, dv, m, 0u, o, o, 1u, 0u);
-    if (gt.n != c || gt.n > GATHER_CAP) return false;
-    sort_list(s.list, gt.n);
-    kmin = key_of(s.list[kk - 1 - (int)cnt_above]);
-    int f0, f1;
-    list_key_range(s.list, 0, (int)gt.n, kmin, f0, f1);
-    st.x_kth = float_of_ord32(kmin);
-    const ListHit hz = list_search(s, s.list, 0, f1 + 1, m, gt.above1, INFINITY);
-    zk = hz.total;
-    nk = cnt_above + (uint32_t)f1 + 1u;
-    kties = f1 - f0 + 1;
+    uint32_t ca;
+    bins_count(s, (uint32_t)g, (uint32_t)kk - s.gabove_cnt[g], klo, kc, ca);
+    kabove = s.gabove_cnt[g] + ca;  // elements in bins above klo
   }
-  st.kord_lo = kmin;
-  st.zk = zk;
 
-  // Windows. The cutoff (top-p, sampling.py:18-25) is the first element of K whose
-  // inclusive mass exceeds tau = p Z_K; it lies in bins [c_lo, c_hi]. Z_P, its inclusive
-  // mass, lies in (tau, tau + its weight], which bounds the draw's target u Z_P; the draw
-  // lies in bins [d_lo, d_hi], at or above c_hi.
-  const bool cut = p < 1.0f;
-  const double tau = (double)p * zk;
-  uint32_t c_lo = 1u, c_hi = 0u;
+  if (topk && kabove + kc <= SMALLK_CAP) {
+    // Everything from the k-th element's bin up fits in one list: the whole row resolves
+    // from it (two passes over the row in all).
+    double a0, a1, a2;
+    const uint32_t ng = gather_bins<DT, 1>(src, s, big, dv, m, klo, 0xffffu, 0u, 0u, 0u, 0u, a0, a1, a2);
+    if (ng != kabove + kc) return false;  // cannot happen: the counts are exact
+    const int n = (int)ng;
+    const Pick pk = list_pick<false>(s, big, n, 0ull, ~0ull, m, 0.0, (double)(kk - 1));
+    if (pk.e == ~0ull) return false;
+    const uint32_t kmin = key_of(pk.e);
+    const uint64_t eK = e_last(kmin);
+    st.x_kth = float_of_ord32(kmin);
+    st.kord_lo = kmin;
+    uint32_t nK, kties;
+    double zq, dummy;
+    list_sum<true>(s, big, n, 0ull, eK, m, nK, zq);
+    list_sum<false>(s, big, n, e_first(kmin), eK, m, kties, dummy);
+    st.zk = zq * FIXQ;
+    uint64_t eD = eK;  // the draw's last candidate
+    if (cut) {
+      const Pick pc = list_pick<true>(s, big, n, 0ull, eK, m, 0.0, (double)p * st.zk);
+      if (pc.e == ~0ull) return false;
+      const uint32_t ckey = key_of(pc.e);
+      uint32_t nkept, ntie, nkeep;
+      list_sum<false>(s, big, n, 0ull, pc.e, m, nkept, dummy);
+      list_sum<false>(s, big, n, e_first(ckey), e_last(ckey), m, ntie, dummy);
+      list_sum<false>(s, big, n, e_first(ckey), pc.e, m, nkeep, dummy);
+      st.x_cut = float_of_ord32(ckey);
+      st.n_cut_tie = (int)ntie;
+      st.n_cut_keep = (int)nkeep;
+      st.n_kept = (int)nkept;
+      st.zp = pc.excl + pc.w;
+      eD = pc.e;
+    } else {
+      st.x_cut = st.x_kth;
+      st.n_cut_tie = st.n_cut_keep = (int)kties;
+      st.n_kept = (int)nK;
+      st.zp = st.zk;
+    }
+    // the draw (sampling.py:26-27, inverse-CDF form)
+    st.target = (double)u * st.zp;
+    const Pick pd = list_pick<true>(s, big, n, 0ull, eD, m, 0.0, st.target);
+    if (pd.e == ~0ull) return false;
+    if (threadIdx.x == 0) write_info(a, b, index_of(pd.e), PBS_ROW_OK, st);
+    return true;
+  }
+
+  // Windows. Z_K lies in [zlo, zhi]: exact (up to rounding) without top-k, bounded by the
+  // bins above klo and the k-th's share of bin klo with it. The cutoff (top-p,
+  // sampling.py:18-25) is the first element of K whose inclusive mass exceeds tau = p Z_K:
+  // in bins [c_lo, c_hi]. Z_P, its inclusive mass, lies in (tau, tau + its weight], which
+  // bounds the draw's target u Z_P (u Z_K without a cutoff): the draw lies in bins
+  // [d_lo, d_hi]. Every window lies at or above klo.
+  double zlo = z_all, zhi = z_all;
+  if (topk) {
+    float wl, wh;
+    bin_bounds(klo, m, wl, wh);
+    zlo = bound_above<false>(s, klo, m) + (double)(kk - (int)kabove) * (double)wl;
+    zhi = bound_above<true>(s, klo, m) + (double)kc * (double)wh;
+  }
+  uint32_t c_lo = 0u, c_hi = 0u;
   double t_lo, t_hi;
   if (cut) {
-    const uint32_t ob = find_bin_bound<true>(s, klo, tau, m);
-    const uint32_t oa = find_bin_bound<false>(s, klo, tau, m);
+    const double tau_lo = (double)p * zlo * (1.0 - 1e-6), tau_hi = (double)p * zhi * (1.0 + 1e-6);
+    const uint32_t ob = find_bin_bound<true>(s, klo, tau_lo, m);
+    const uint32_t oa = find_bin_bound<false>(s, klo, tau_hi, m);
     c_lo = min(oa, ob);
     c_hi = max(oa, ob);
     float wl, wh;
     bin_bounds(c_hi, m, wl, wh);
-    t_lo = (double)u * tau * (1.0 - 1e-6);
-    t_hi = (double)u * (tau + (double)wh) * (1.0 + 1e-6);
+    t_lo = (double)u * tau_lo * (1.0 - 1e-6);
+    t_hi = (double)u * (tau_hi + (double)wh) * (1.0 + 1e-6);
   } else {
-    t_lo = (double)u * zk * (1.0 - 1e-6);
-    t_hi = (double)u * zk * (1.0 + 1e-6);
+    t_lo = (double)u * zlo * (1.0 - 1e-6);
+    t_hi = (double)u * zhi * (1.0 + 1e-6);
   }
   const uint32_t d_hi = find_bin_bound<true>(s, klo, t_lo, m);
   const uint32_t d_lo = find_bin_bound<false>(s, klo, t_hi, m);
-  // window 1 holds the draw's bins (and the cutoff's when they meet); window 2 the cutoff's
-  uint32_t lo1 = d_lo, hi1 = d_hi, lo2 = 1u, hi2 = 0u;
-  if (cut) {
-    if (d_lo <= c_hi + 1u) {
-      lo1 = min(d_lo, c_lo);
-      hi1 = max(d_hi, c_hi);
-    } else {
-      lo2 = c_lo;
-      hi2 = c_hi;
-    }
-  }
-  const bool split = lo2 <= hi2;
-  // elements above the list's cutoff segment (all in K: the windows lie at or above klo)
-  const uint32_t n_above_seg = cut ? count_bins_ge(s, (split ? hi2 : hi1) + 1u) : 0u;
+  const uint32_t dlo = min(d_lo, d_hi), dhi = max(d_lo, d_hi);
+  // every element above the cutoff window is in K (the window lies at or above klo)
+  const uint32_t n_above_c = cut ? count_bins_ge(s, c_hi + 1u) : 0u;
   const uint32_t n_neg_inf = hist_count(s, ord32(-INFINITY) >> 16);
-  const Gathered gw = gather_bins<DT>(src, s, big, LIST_CAP, dv, m, kmin, lo1, hi1, lo2, hi2);
-  if (gw.n > LIST_CAP) return false;
-  sort_list(big, gw.n);
-  const int n = (int)gw.n, n1 = (int)gw.n1;
-  const int cs0 = split ? n1 : 0;  // the cutoff's segment of the list and the mass above it
-  const double cbase = split ? gw.above2 : gw.above1;
-  int dend = n;                     // the draw searches [0, dend) of window 1 ...
-  int cpos = n - 1;
-  if (cut) {
-    const ListHit hc = list_search(s, big, cs0, n, m, cbase, tau);
-    if (hc.pos < 0) return false;
-    const uint32_t ckey = key_of(big[hc.pos]);
-    int c0, c1;
-    list_key_range(big, cs0, n, ckey, c0, c1);
-    st.x_cut = float_of_ord32(ckey);
-    st.n_cut_tie = c1 - c0 + 1;
-    st.n_cut_keep = hc.pos - c0 + 1;
-    st.zp = hc.excl + hc.w;
-    st.n_kept = (int)n_above_seg + (hc.pos - cs0) + 1;
-    cpos = hc.pos;
-    dend = split ? n1 : hc.pos + 1;
+  // windows: the draw's, then the cutoff's and the k-th element's bin when they apply
+  double above_d, above_c = 0.0, above_k = 0.0, a2;
+  uint32_t ng;
+  if (cut && topk) ng = gather_bins<DT, 3>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, klo, klo, above_d, above_c, above_k);
+  else if (cut) ng = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, 0u, 0u, above_d, above_c, a2);
+  else if (topk) ng = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, klo, klo, 0u, 0u, above_d, above_k, a2);
+  else ng = gather_bins<DT, 1>(src, s, big, dv, m, dlo, dhi, 0u, 0u, 0u, 0u, above_d, a2, a2);
+  if (ng > LIST_CAP) return false;
+  const int n = (int)ng;
+  double dummy;
+
+  uint64_t eK = ~0ull;  // last entry of K
+  double zk = z_all;
+  uint32_t nk = (uint32_t)V;
+  if (topk) {
+    const Pick pk = list_pick<false>(s, big, n, e_bins_first(klo), e_bins_last(klo), m, 0.0,
+                                     (double)(kk - 1 - (int)kabove));
+    if (pk.e == ~0ull) return false;
+    const uint32_t kmin = key_of(pk.e);
+    eK = e_last(kmin);
+    st.x_kth = float_of_ord32(kmin);
+    st.kord_lo = kmin;
+    uint32_t cnt, kties;
+    double zq;
+    // Z_K: the mass above bin klo, plus its entries down to the last of K
+    list_sum<true>(s, big, n, e_bins_first(klo), eK, m, cnt, zq);
+    zk = above_k + zq * FIXQ;
+    nk = kabove + cnt;
+    list_sum<false>(s, big, n, e_first(kmin), eK, m, kties, dummy);
+    st.x_cut = st.x_kth;
+    st.n_cut_tie = st.n_cut_keep = (int)kties;
   } else {
-    st.zp = zk;
-    st.n_kept = (int)nk;
-    if (topk) {
-      st.x_cut = st.x_kth;
-      st.n_cut_tie = st.n_cut_keep = kties;
-    } else {
-      // every element is kept: the lowest "cutoff" value is -inf, with all its ties
-      st.x_cut = -INFINITY;
-      st.n_cut_tie = st.n_cut_keep = (int)n_neg_inf;
-    }
+    // every element is kept: the lowest "cutoff" value is -inf, with all its ties
+    st.x_cut = -INFINITY;
+    st.n_cut_tie = st.n_cut_keep = (int)n_neg_inf;
   }
-  // the draw (sampling.py:26-27, inverse-CDF form): in window 1, or in the cutoff's
-  // segment, up to the cutoff, when the target lies at or past the mass above it
+  st.zk = zk;
+  st.zp = zk;
+  st.n_kept = (int)nk;
+
+  uint64_t ec = ~0ull;  // the cutoff's entry
+  if (cut) {
+    const uint64_t ea = e_bins_first(c_hi);
+    const Pick pc = list_pick<true>(s, big, n, ea, min_u64(e_bins_last(c_lo), eK), m, above_c, (double)p * zk);
+    if (pc.e == ~0ull) return false;
+    ec = pc.e;
+    const uint32_t ckey = key_of(ec);
+    uint32_t cnt, ntie, nkeep;
+    list_sum<false>(s, big, n, ea, ec, m, cnt, dummy);
+    list_sum<false>(s, big, n, e_first(ckey), e_last(ckey), m, ntie, dummy);
+    list_sum<false>(s, big, n, e_first(ckey), ec, m, nkeep, dummy);
+    st.x_cut = float_of_ord32(ckey);
+    st.n_cut_tie = (int)ntie;
+    st.n_cut_keep = (int)nkeep;
+    st.n_kept = (int)(n_above_c + cnt);
+    st.zp = pc.excl + pc.w;
+  }
+  // the draw (sampling.py:26-27, inverse-CDF form): in the cutoff window, up to the
+  // cutoff, when the target lies at or past the mass above that window; else in the draw
+  // window
   const double t = (double)u * st.zp;
   st.target = t;
-  const ListHit hd = (split && t >= gw.above2) ? list_search(s, big, n1, cpos + 1, m, gw.above2, t)
-                                               : list_search(s, big, 0, dend, m, gw.above1, t);
-  if (hd.pos < 0) return false;
-  if (threadIdx.x == 0) write_info(a, b, index_of(big[hd.pos]), PBS_ROW_OK, st);
+  const bool in_c = cut && t >= above_c;
+  const uint64_t first = e_bins_first(in_c ? c_hi : dhi);
+  const uint64_t last = min_u64(min_u64(e_bins_last(in_c ? c_lo : dlo), eK), ec);
+  const Pick pd = list_pick<true>(s, big, n, first, last, m, in_c ? above_c : above_d, t);
+  if (pd.e == ~0ull) return false;
+  if (threadIdx.x == 0) write_info(a, b, index_of(pd.e), PBS_ROW_OK, st);
   return true;
 }
 
@@ -2332,7 +2405,11 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
       if (sample_row16<DT>(a, s, src, b, T, kk, p, u)) return;
       m = bis_max<DT>(mem, s, dv, false);
     } else {
-      if (sample_row32<DT>(a, s, src, mem, b, dv, kk, p, u, m)) return;
+      if (T == 1.0f) {
+        if (sample_row32<DT>(a, s, src, mem, b, UnitDivider{}, kk, p, u, m)) return;
+      } else {
+        if (sample_row32<DT>(a, s, src, mem, b, dv, kk, p, u, m)) return;
+      }
     }
     sample_row_bisect<DT>(a, s, mem, b, m, dv, kk, p, u);
   } else {
@@ -2341,7 +2418,11 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
       if (sample_row16<DT>(a, s, src, b, T, kk, p, u)) return;
       m = bis_max<DT>(src, s, dv, false);
     } else {
-      if (sample_row32<DT>(a, s, src, src, b, dv, kk, p, u, m)) return;
+      if (T == 1.0f) {
+        if (sample_row32<DT>(a, s, src, src, b, UnitDivider{}, kk, p, u, m)) return;
+      } else {
+        if (sample_row32<DT>(a, s, src, src, b, dv, kk, p, u, m)) return;
+      }
     }
     sample_row_bisect<DT>(a, s, src, b, m, dv, kk, p, u);
   }
