@@ -388,7 +388,7 @@ struct __align__(16) Smem {
       uint32_t bcnt[NBUCKET];     //   and entries per bucket
     } f32;
   };
-  uint32_t list_n;               // fp32 rows: entries gathered
+  uint32_t seg_n[NWAVE];         // fp32 rows: entries each wave gathered into its list segment
   uint64_t pick;                 // fp32 rows: the entry a list search found
   uint32_t cand[NWAVE], cand_cnt[NWAVE], last[NWAVE], last_cnt[NWAVE];  // list searches, per wave
   double cand_excl[NWAVE], last_excl[NWAVE];
@@ -1696,6 +1696,7 @@ __device__ __forceinline__ void sample_row_bisect(const KArgs& a, Smem& s, const
 // bisection path.
 // ---------------------------------------------------------------------------------------
 constexpr uint32_t LIST_CAP = HIST_WORDS / 2;  // entries of the list, which reuses the histogram
+constexpr uint32_t SEG = LIST_CAP / NWAVE;     // list segment of each wave
 constexpr uint32_t SMALLK_CAP = 4096;          // top-k rows resolved from one list up to this size
 constexpr float LOG2E_F = 1.44269504088896341f;
 constexpr double FIXQ = 0x1p-38;               // fixed-point weight unit
@@ -1830,16 +1831,17 @@ __device__ __forceinline__ uint32_t find_bin_bound(const Smem& s, uint32_t lo, d
 
 // One pass over the row: every element whose bin lies in one of the NW windows [lo_i,
 // hi_i] (they may overlap) goes into L, unsorted; above_i gets the exact mass of the
-// elements in bins above window i. Returns the number of entries (more than LIST_CAP: the
-// list holds only some).
+// elements in bins above window i. Each wave appends to its own segment of SEG entries
+// (ballot and lane rank: no atomics). Returns false if a segment overflowed.
 template <int DT, int NW, class Src, class Div>
-__device__ __forceinline__ uint32_t gather_bins(const Src& src, Smem& s, uint64_t* L, const Div& dv, float m,
+__device__ __forceinline__ bool gather_bins(const Src& src, Smem& s, uint64_t* L, const Div& dv, float m,
                                                 uint32_t lo0, uint32_t hi0, uint32_t lo1, uint32_t hi1,
                                                 uint32_t lo2, uint32_t hi2, double& above0, double& above1,
                                                 double& above2) {
   const uint32_t lo[3] = {lo0, lo1, lo2}, hi[3] = {hi0, hi1, hi2};
-  if (threadIdx.x == 0) s.list_n = 0u;
-  __syncthreads();
+  uint64_t* const seg = L + wave_id() * SEG;
+  uint32_t wn = 0u;  // entries the wave appended (uniform)
+  __syncthreads();   // the histogram the list overwrites is no longer read
   double acc[NW];
 #pragma unroll
   for (int r = 0; r < NW; ++r) acc[r] = 0.0;
@@ -1860,9 +1862,12 @@ __device__ __forceinline__ uint32_t gather_bins(const Src& src, Smem& s, uint64_
         part[r] += (o > hi[r]) ? w : 0.0f;
         in = in || (o - lo[r] <= hi[r] - lo[r]);
       }
-      if (ok && in) {
-        const uint32_t slot = atomicAdd(&s.list_n, 1u);
-        if (slot < LIST_CAP) L[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
+      const uint64_t bal = ballot(ok && in);
+      if (bal) {
+        const uint32_t slot = wn + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (ok && in && slot < SEG) seg[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
+        wn += (uint32_t)__popcll(bal);
       }
     }
 #pragma unroll
@@ -1881,19 +1886,25 @@ __device__ __forceinline__ uint32_t gather_bins(const Src& src, Smem& s, uint64_
   above0 = tot[0];
   above1 = tot[1];
   above2 = tot[2];
-  const uint32_t n = s.list_n;
+  if (lane_id() == 0) s.seg_n[wave_id()] = wn;
   __syncthreads();
-  return n;
+  bool ok = true;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) ok = ok && s.seg_n[w] <= SEG;
+  return ok;
 }
 
-// count and fixed-point mass (FIXQ units, exact) of the entries of L[0, n) in [ea, eb]
+// count and fixed-point mass (FIXQ units, exact) of the list's entries in [ea, eb]; each
+// wave reads its own segment
 template <bool MASS>
-__device__ __forceinline__ void list_sum(Smem& s, const uint64_t* L, int n, uint64_t ea, uint64_t eb, float m,
+__device__ __forceinline__ void list_sum(Smem& s, const uint64_t* L, uint64_t ea, uint64_t eb, float m,
                                          uint32_t& cnt, double& mass) {
   uint32_t c = 0u;
   uint64_t q = 0u;
-  for (int i = threadIdx.x; i < n; i += NT) {
-    const uint64_t e = L[i];
+  const uint64_t* const seg = L + wave_id() * SEG;
+  const int sn = (int)s.seg_n[wave_id()];
+  for (int i = lane_id(); i < sn; i += 64) {
+    const uint64_t e = seg[i];
     if (e >= ea && e <= eb) {
       ++c;
       if (MASS) q += fixq(wexp(value_of(e), m));
@@ -1922,15 +1933,17 @@ struct Pick {
   double w;     // its weight (fixed-point, as the cumulative counts it)
 };
 
-// The first entry of L[0, n) in [ea, eb], in ascending order, whose inclusive cumulative
+// The first entry of the list in [ea, eb], in ascending order, whose inclusive cumulative
 // from `base` exceeds target: weights are the entries' fixed-point masses (MASS) or 1 (a
 // count). If none does, the last entry with weight. Each level spreads the interval over
 // NBUCKET buckets, sums them exactly and keeps the bucket where the cumulative crosses,
 // until one entry is left.
 template <bool MASS>
-__device__ __forceinline__ Pick list_pick(Smem& s, const uint64_t* L, int n, uint64_t ea, uint64_t eb, float m,
+__device__ __forceinline__ Pick list_pick(Smem& s, const uint64_t* L, uint64_t ea, uint64_t eb, float m,
                                           double base, double target) {
   const int t = threadIdx.x, l = lane_id(), wv = wave_id();
+  const uint64_t* const seg = L + wv * SEG;
+  const int sn = (int)s.seg_n[wv];
   const double unit = MASS ? FIXQ : 1.0;
   uint64_t lo = ea, hi = eb;
   double B = base;
@@ -1944,8 +1957,8 @@ __device__ __forceinline__ Pick list_pick(Smem& s, const uint64_t* L, int n, uin
       s.f32.bcnt[t] = 0u;
     }
     __syncthreads();
-    for (int i = t; i < n; i += NT) {
-      const uint64_t e = L[i];
+    for (int i = l; i < sn; i += 64) {
+      const uint64_t e = seg[i];
       if (e >= lo && e <= hi) {
         const uint32_t bk = (uint32_t)((e - lo) >> sh);
         atomicAdd(&s.f32.bcnt[bk], 1u);
@@ -2023,8 +2036,8 @@ __device__ __forceinline__ Pick list_pick(Smem& s, const uint64_t* L, int n, uin
   // the interval now holds one entry (or one value of E)
   if (t == 0) s.pick = ~0ull;
   __syncthreads();
-  for (int i = t; i < n; i += NT) {
-    const uint64_t e = L[i];
+  for (int i = l; i < sn; i += 64) {
+    const uint64_t e = seg[i];
     if (e >= lo && e <= hi) s.pick = e;
   }
   __syncthreads();
@@ -2187,10 +2200,8 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     // Everything from the k-th element's bin up fits in one list: the whole row resolves
     // from it (two passes over the row in all).
     double a0, a1, a2;
-    const uint32_t ng = gather_bins<DT, 1>(src, s, big, dv, m, klo, 0xffffu, 0u, 0u, 0u, 0u, a0, a1, a2);
-    if (ng != kabove + kc) return false;  // cannot happen: the counts are exact
-    const int n = (int)ng;
-    const Pick pk = list_pick<false>(s, big, n, 0ull, ~0ull, m, 0.0, (double)(kk - 1));
+    if (!gather_bins<DT, 1>(src, s, big, dv, m, klo, 0xffffu, 0u, 0u, 0u, 0u, a0, a1, a2)) return false;
+    const Pick pk = list_pick<false>(s, big, 0ull, ~0ull, m, 0.0, (double)(kk - 1));
     if (pk.e == ~0ull) return false;
     const uint32_t kmin = key_of(pk.e);
     const uint64_t eK = e_last(kmin);
@@ -2198,18 +2209,18 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     st.kord_lo = kmin;
     uint32_t nK, kties;
     double zq, dummy;
-    list_sum<true>(s, big, n, 0ull, eK, m, nK, zq);
-    list_sum<false>(s, big, n, e_first(kmin), eK, m, kties, dummy);
+    list_sum<true>(s, big, 0ull, eK, m, nK, zq);
+    list_sum<false>(s, big, e_first(kmin), eK, m, kties, dummy);
     st.zk = zq * FIXQ;
     uint64_t eD = eK;  // the draw's last candidate
     if (cut) {
-      const Pick pc = list_pick<true>(s, big, n, 0ull, eK, m, 0.0, (double)p * st.zk);
+      const Pick pc = list_pick<true>(s, big, 0ull, eK, m, 0.0, (double)p * st.zk);
       if (pc.e == ~0ull) return false;
       const uint32_t ckey = key_of(pc.e);
       uint32_t nkept, ntie, nkeep;
-      list_sum<false>(s, big, n, 0ull, pc.e, m, nkept, dummy);
-      list_sum<false>(s, big, n, e_first(ckey), e_last(ckey), m, ntie, dummy);
-      list_sum<false>(s, big, n, e_first(ckey), pc.e, m, nkeep, dummy);
+      list_sum<false>(s, big, 0ull, pc.e, m, nkept, dummy);
+      list_sum<false>(s, big, e_first(ckey), e_last(ckey), m, ntie, dummy);
+      list_sum<false>(s, big, e_first(ckey), pc.e, m, nkeep, dummy);
       st.x_cut = float_of_ord32(ckey);
       st.n_cut_tie = (int)ntie;
       st.n_cut_keep = (int)nkeep;
@@ -2224,7 +2235,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     }
     // the draw (sampling.py:26-27, inverse-CDF form)
     st.target = (double)u * st.zp;
-    const Pick pd = list_pick<true>(s, big, n, 0ull, eD, m, 0.0, st.target);
+    const Pick pd = list_pick<true>(s, big, 0ull, eD, m, 0.0, st.target);
     if (pd.e == ~0ull) return false;
     if (threadIdx.x == 0) write_info(a, b, index_of(pd.e), PBS_ROW_OK, st);
     return true;
@@ -2267,20 +2278,19 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   const uint32_t n_neg_inf = hist_count(s, ord32(-INFINITY) >> 16);
   // windows: the draw's, then the cutoff's and the k-th element's bin when they apply
   double above_d, above_c = 0.0, above_k = 0.0, a2;
-  uint32_t ng;
-  if (cut && topk) ng = gather_bins<DT, 3>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, klo, klo, above_d, above_c, above_k);
-  else if (cut) ng = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, 0u, 0u, above_d, above_c, a2);
-  else if (topk) ng = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, klo, klo, 0u, 0u, above_d, above_k, a2);
-  else ng = gather_bins<DT, 1>(src, s, big, dv, m, dlo, dhi, 0u, 0u, 0u, 0u, above_d, a2, a2);
-  if (ng > LIST_CAP) return false;
-  const int n = (int)ng;
+  bool fits;
+  if (cut && topk) fits = gather_bins<DT, 3>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, klo, klo, above_d, above_c, above_k);
+  else if (cut) fits = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, 0u, 0u, above_d, above_c, a2);
+  else if (topk) fits = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, klo, klo, 0u, 0u, above_d, above_k, a2);
+  else fits = gather_bins<DT, 1>(src, s, big, dv, m, dlo, dhi, 0u, 0u, 0u, 0u, above_d, a2, a2);
+  if (!fits) return false;
   double dummy;
 
   uint64_t eK = ~0ull;  // last entry of K
   double zk = z_all;
   uint32_t nk = (uint32_t)V;
   if (topk) {
-    const Pick pk = list_pick<false>(s, big, n, e_bins_first(klo), e_bins_last(klo), m, 0.0,
+    const Pick pk = list_pick<false>(s, big, e_bins_first(klo), e_bins_last(klo), m, 0.0,
                                      (double)(kk - 1 - (int)kabove));
     if (pk.e == ~0ull) return false;
     const uint32_t kmin = key_of(pk.e);
@@ -2290,10 +2300,10 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     uint32_t cnt, kties;
     double zq;
     // Z_K: the mass above bin klo, plus its entries down to the last of K
-    list_sum<true>(s, big, n, e_bins_first(klo), eK, m, cnt, zq);
+    list_sum<true>(s, big, e_bins_first(klo), eK, m, cnt, zq);
     zk = above_k + zq * FIXQ;
     nk = kabove + cnt;
-    list_sum<false>(s, big, n, e_first(kmin), eK, m, kties, dummy);
+    list_sum<false>(s, big, e_first(kmin), eK, m, kties, dummy);
     st.x_cut = st.x_kth;
     st.n_cut_tie = st.n_cut_keep = (int)kties;
   } else {
@@ -2308,14 +2318,14 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   uint64_t ec = ~0ull;  // the cutoff's entry
   if (cut) {
     const uint64_t ea = e_bins_first(c_hi);
-    const Pick pc = list_pick<true>(s, big, n, ea, min_u64(e_bins_last(c_lo), eK), m, above_c, (double)p * zk);
+    const Pick pc = list_pick<true>(s, big, ea, min_u64(e_bins_last(c_lo), eK), m, above_c, (double)p * zk);
     if (pc.e == ~0ull) return false;
     ec = pc.e;
     const uint32_t ckey = key_of(ec);
     uint32_t cnt, ntie, nkeep;
-    list_sum<false>(s, big, n, ea, ec, m, cnt, dummy);
-    list_sum<false>(s, big, n, e_first(ckey), e_last(ckey), m, ntie, dummy);
-    list_sum<false>(s, big, n, e_first(ckey), ec, m, nkeep, dummy);
+    list_sum<false>(s, big, ea, ec, m, cnt, dummy);
+    list_sum<false>(s, big, e_first(ckey), e_last(ckey), m, ntie, dummy);
+    list_sum<false>(s, big, e_first(ckey), ec, m, nkeep, dummy);
     st.x_cut = float_of_ord32(ckey);
     st.n_cut_tie = (int)ntie;
     st.n_cut_keep = (int)nkeep;
@@ -2330,7 +2340,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   const bool in_c = cut && t >= above_c;
   const uint64_t first = e_bins_first(in_c ? c_hi : dhi);
   const uint64_t last = min_u64(min_u64(e_bins_last(in_c ? c_lo : dlo), eK), ec);
-  const Pick pd = list_pick<true>(s, big, n, first, last, m, in_c ? above_c : above_d, t);
+  const Pick pd = list_pick<true>(s, big, first, last, m, in_c ? above_c : above_d, t);
   if (pd.e == ~0ull) return false;
   if (threadIdx.x == 0) write_info(a, b, index_of(pd.e), PBS_ROW_OK, st);
   return true;
