@@ -59,6 +59,7 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------------------
 constexpr int ROW_SHR1 = 0x111, ROW_SHR2 = 0x112, ROW_SHR4 = 0x114, ROW_SHR8 = 0x118;
 constexpr int ROW_BCAST15 = 0x142, ROW_BCAST31 = 0x143;
+constexpr int ROW_ROR8 = 0x128, ROW_HALF_MIRROR = 0x141, QUAD_XOR1 = 0xb1, QUAD_XOR2 = 0x4e;
 
 template <int CTRL, int RM = 0xf>
 __device__ __forceinline__ uint32_t dpp(uint32_t v, uint32_t old) {
@@ -725,8 +726,10 @@ __device__ __forceinline__ int select_index(const Src& src, Smem& s, M&& match, 
 // whose key lies in [lo, lo + span]. The key is the raw 16-bit pattern (ORD = false: a
 // range of values of one sign is a contiguous range of raws) or the unfolded ord (ORD =
 // true: ranges that take in both -0 and +0). Per-(chunk, wave) match counts locate the
-// answer (exact counts only where a wave has a match in the chunk); only the wave holding
-// it then looks at its lanes.
+// answer: every lane counts its matches in each chunk with packed 16-bit ops, and one
+// transposed reduction across the wave leaves each chunk's total in a known lane (no
+// branch or scalar dependency per chunk); only the wave holding the answer then looks at
+// its lanes.
 __device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
 }
@@ -748,38 +751,122 @@ __device__ __forceinline__ uint32_t match_bits16(const u4& q, uint32_t lo2, uint
   return bits;
 }
 
+// Elements of one 16-byte vector whose key is NOT in [lo, lo + span]: a half of
+// key - lo (mod 2^16) that is <= span becomes 0 (xor when span == 0, saturating
+// subtraction otherwise), min(., 1) marks the others, packed adds and one dot product with
+// (1, 1) count them. `one2` is (1, 1) held opaque by the caller.
+template <bool ORD, bool EXACT>
+__device__ __forceinline__ uint32_t lane_misses16(const u4& q, uint32_t lo2, uint32_t span2, uint32_t one2) {
+  uint32_t m[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t x;
+    if constexpr (EXACT) {
+      x = key16x2<ORD>(q[d]) ^ lo2;
+    } else {
+      x = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(
+                                           __builtin_bit_cast(u16x2, pk_sub_u16(key16x2<ORD>(q[d]), lo2)),
+                                           __builtin_bit_cast(u16x2, span2)));
+    }
+    m[d] = pk_min_u16(x, one2);
+  }
+  const uint32_t s = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, m[0]) + __builtin_bit_cast(u16x2, m[1]) +
+                                                      (__builtin_bit_cast(u16x2, m[2]) + __builtin_bit_cast(u16x2, m[3])));
+  return add_u16_pair(s, 0u);
+}
+
+// Wave totals of 32 per-lane counters held as 16 packed u16 pairs (pair r = counters 2r,
+// 2r + 1; every total fits 16 bits). Each stage halves the pairs a lane carries and sums
+// it with a partner lane: lane bit 5 (permlane32 swap), bit 4 (permlane16 swap), bit 3
+// (row rotate by 8), bit 2 (half-row mirror) pick the pair kept, then the quad sums. Lane l
+// ends with the totals of pair (l >> 2) & 15.
+__device__ __forceinline__ uint32_t wave_totals16(const uint32_t (&P)[16]) {
+  const int l = lane_id();
+  uint32_t s1[8], s2[4], s3[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(P[i], P[i + 8], false, false);
+    s1[i] = r[0] + r[1];  // lanes 0-31: pair i, lanes 32-63: pair i + 8
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(s1[i], s1[i + 4], false, false);
+    s2[i] = r[0] + r[1];  // odd 16-lane rows: pair + 4
+  }
+  const bool b3 = (l & 8) != 0, b2 = (l & 4) != 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t keep = b3 ? s2[i + 2] : s2[i], send = b3 ? s2[i] : s2[i + 2];
+    s3[i] = keep + dpp<ROW_ROR8>(send, 0u);
+  }
+  const uint32_t keep = b2 ? s3[1] : s3[0], send = b2 ? s3[0] : s3[1];
+  uint32_t t = keep + dpp<ROW_HALF_MIRROR>(send, 0u);
+  t += dpp<QUAD_XOR1>(t, 0u);
+  t += dpp<QUAD_XOR2>(t, 0u);
+  return t;
+}
+
+// r[j] for a run-time (wave-uniform) j < N by a chain of selects: one vector live, not N.
+// Each vector first passes through an empty asm statement: as plain loads from the row
+// array the selects would be folded into one indexed load, moving the row to scratch.
+template <int N>
+__device__ __forceinline__ u4 pick_chunk(const u4 (&r)[N], int j) {
+  u4 q = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    uint32_t a = r[i].x, b = r[i].y, c = r[i].z, d = r[i].w;
+    asm("" : "+v"(a));
+    asm("" : "+v"(b));
+    asm("" : "+v"(c));
+    asm("" : "+v"(d));
+    if (i == j) q = (u4){a, b, c, d};
+  }
+  return q;
+}
+
 template <bool ORD, int DT, int NCH>
 __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Smem& s, uint32_t lo, uint32_t span,
                                                   int rank) {
-  static_assert(NCH * NWAVE <= 256, "chunk table must fit 4 entries per lane");
+  static_assert(NCH * NWAVE <= 256 && NCH <= 32, "chunk table must fit 4 entries per lane");
   const int l = lane_id(), w = wave_id();
   const uint32_t lo2 = lo | (lo << 16);
-  const u16x2 lo2v = __builtin_bit_cast(u16x2, lo2);
-  const u16x2 span2v = __builtin_bit_cast(u16x2, span | (span << 16));
+  {
+    const uint32_t span2 = span | (span << 16);
+    // (1, 1) through an empty asm: with a visible constant the compiler rewrites the packed
+    // min(x, 1) as two compares and two selects
+    uint32_t one2 = 0x00010001u;
+    asm("" : "+v"(one2));
+    // per-lane misses of the valid vectors, chunks 2r and 2r + 1 packed in P[r]
+    uint32_t P[16];
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const uint64_t vmask = ballot(j * NT + (int)threadIdx.x < src.nvec);
-    // Does any of the lane's 8 elements match? key - lo (mod 2^16) <= span is a zero after
-    // a saturating subtraction of span; the minimum over the halves finds one. About
-    // three packed VALU ops per 16-bit pair, one compare per chunk, no scalar chains.
-    u16x2 mn = {0xffffu, 0xffffu};
+    for (int r = 0; r < 16; ++r) P[r] = 0u;
+    if (span == 0u) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const u16x2 dl = __builtin_bit_cast(u16x2, key16x2<ORD>(src.r[j][d])) - lo2v;
-      mn = __builtin_elementwise_min(mn, __builtin_elementwise_sub_sat(dl, span2v));
-    }
-    const uint64_t any = __builtin_amdgcn_uicmp((uint32_t)min(mn.x, mn.y), 0u, 32 /* eq */) & vmask;
-    uint32_t c = 0;
-    if (any) {
-      // rare: the exact count of this chunk's matches in the wave
+      for (int j = 0; j < NCH; ++j) {
+        const uint32_t c = lane_misses16<ORD, true>(src.r[j], lo2, span2, one2);
+        P[j >> 1] |= (j * NT + (int)threadIdx.x < src.nvec ? c : 0u) << (16 * (j & 1));
+      }
+    } else {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t dl = pk_sub_u16(key16x2<ORD>(src.r[j][d]), lo2);
-        c += (uint32_t)__popcll(__builtin_amdgcn_uicmp(dl & 0xffffu, span, 37 /* ule */) & vmask);
-        c += (uint32_t)__popcll(__builtin_amdgcn_uicmp(dl >> 16, span, 37 /* ule */) & vmask);
+      for (int j = 0; j < NCH; ++j) {
+        const uint32_t c = lane_misses16<ORD, false>(src.r[j], lo2, span2, one2);
+        P[j >> 1] |= (j * NT + (int)threadIdx.x < src.nvec ? c : 0u) << (16 * (j & 1));
       }
     }
-    if (l == 0) s.hist[j * NWAVE + w] = c;
+    const uint32_t t = wave_totals16(P);
+    if ((l & 3) == 0) {
+      // matches = 8 per valid lane of the (chunk, wave) minus its misses
+      const int r = l >> 2;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = 2 * r + h;
+        if (j < NCH) {
+          const int first = j * NT + w * 64;
+          const int nlanes = min(64, max(0, src.nvec - first));
+          s.hist[j * NWAVE + w] = 8u * (uint32_t)nlanes - ((t >> (16 * h)) & 0xffffu);
+        }
+      }
+    }
   }
   __syncthreads();
   if (w == 0) {
@@ -819,11 +906,7 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
   if (pos >= 0) {
     const int jstar = pos / NWAVE, wstar = pos % NWAVE, rr = s.sel_rank;
     if (w == wstar) {
-      // chunk jstar by a select chain on the (wave-uniform) index: one vector live, not NCH
-      u4 q = src.r[0];
-#pragma unroll
-      for (int j = 1; j < NCH; ++j)
-        if (j == jstar) q = src.r[j];
+      const u4 q = pick_chunk<NCH>(src.r, jstar);
       const uint32_t bits = (jstar * NT + (int)threadIdx.x < src.nvec) ? match_bits16<ORD>(q, lo2, span) : 0u;
       const uint32_t cnt = (uint32_t)__popc(bits);
       const uint32_t incl = wscan_u32(cnt);
@@ -1278,6 +1361,8 @@ __device__ __forceinline__ bool resolve16(const Smem& s, int V, const Divider& d
 // Index of the rank-th lowest-index element whose ord lies in [lo, hi].
 template <int DT, class Src>
 __device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank) {
+  // the searches before this read the histogram wave by wave; the selection reuses it
+  __syncthreads();
   if constexpr (Src::kStore) {
     // values of one sign: a contiguous range of raws (non-negative ords lo.. map to raws
     // lo - 0x8000.., negative ones to raws 0xffff - hi ..)
