@@ -374,6 +374,16 @@ struct RowState {
   double zk, zp, target;
 };
 
+// A tie group located by a search (16-bit rows): its ord range, count, mass above it and
+// per-element weight.
+struct TieGroup {
+  uint32_t lo, hi;
+  uint32_t n;        // elements with ord in [lo, hi]
+  uint32_t n_above;  // elements above hi
+  double above;      // mass above hi
+  double w;          // weight of one element
+};
+
 struct __align__(16) Smem {
   uint32_t hist[HIST_WORDS];     // 16-bit rows: packed u16 count per raw pattern; reused by index selection
   uint32_t gcount[NGROUP];       // count of each group of 256 ords
@@ -400,6 +410,8 @@ struct __align__(16) Smem {
   uint32_t nan_cnt;              // 16-bit rows: elements in the NaN / inf raw blocks
 
   int sel_jstar, sel_rank, sel_index;
+  TieGroup spec[2];              // 16-bit rows: cutoff and guessed draw, searched side by side
+  int spec_ok[2];
   RowState st;
 };
 
@@ -1244,16 +1256,6 @@ __device__ __forceinline__ void count_mass_ge(const Smem& s, uint32_t t, const D
   mass = wsum_f64(w) + s.gabove_mass[g];
 }
 
-// A tie group located by a search: its ord range, count, mass above it and per-element
-// weight.
-struct TieGroup {
-  uint32_t lo, hi;
-  uint32_t n;        // elements with ord in [lo, hi]
-  uint32_t n_above;  // elements above hi
-  double above;      // mass above hi
-  double w;          // weight of one element
-};
-
 template <int DT>
 __device__ __forceinline__ TieGroup tie_group(const Smem& s, const BinHit& h, uint32_t range_lo, const Divider& dv,
                                               float m) {
@@ -1276,11 +1278,12 @@ __device__ __forceinline__ TieGroup tie_group(const Smem& s, const BinHit& h, ui
 }
 
 // Top-k threshold, top-p cutoff and draw position from the histogram summaries. Every
-// wave runs it (the searches are wave-local) and ends with the same RowState. Returns false
-// if a u16 counter wrapped (one value more than 65535 times): the caller then takes the
-// general path.
+// wave runs it and ends with the same RowState. The searches are wave-local, except that
+// with top-p the cutoff and a guessed draw run side by side on the two halves of the
+// waves (one barrier). Returns false if a u16 counter wrapped (one value more than 65535
+// times): the caller then takes the general path.
 template <int DT>
-__device__ __forceinline__ bool resolve16(const Smem& s, int V, const Divider& dv, int kk, float p, float u, float m,
+__device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int kk, float p, float u, float m,
                                           bool want_info, RowState& st) {
   const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
   if (total_cnt != (uint32_t)V) return false;
@@ -1307,14 +1310,31 @@ __device__ __forceinline__ bool resolve16(const Smem& s, int V, const Divider& d
   }
   st.zk = zk;
 
-  // top-p (sampling.py:18-25): keep the shortest prefix whose exclusive mass is <= p * Z_K
+  // top-p (sampling.py:18-25): keep the shortest prefix whose exclusive mass is <= p * Z_K.
+  // Z_P lies in (tau, tau + one weight], so the draw's target u Z_P is close to u tau: the
+  // first half of the waves searches the cutoff while the second half searches the draw
+  // for u tau; the guess is kept below if u Z_P falls in the tie group it found.
   TieGroup ct = kt;
   int n_keep;
   double zp;
   const double tau = (double)p * zk;
-  const bool cut = p < 1.0f && find_by_mass<DT>(s, k_lo, tau, dv, m, h);
+  bool cut = false, have_guess = false;
+  TieGroup guess = {};
+  if (p < 1.0f) {
+    const bool second = wave_id() >= NWAVE / 2;
+    const bool ok = find_by_mass<DT>(s, k_lo, second ? (double)u * tau : tau, dv, m, h);
+    const TieGroup tg = ok ? tie_group<DT>(s, h, k_lo, dv, m) : TieGroup{};
+    if (lane_id() == 0 && (wave_id() == 0 || wave_id() == NWAVE / 2)) {
+      s.spec[second ? 1 : 0] = tg;
+      s.spec_ok[second ? 1 : 0] = ok ? 1 : 0;
+    }
+    __syncthreads();
+    cut = s.spec_ok[0] != 0;
+    have_guess = s.spec_ok[1] != 0;
+    if (cut) ct = s.spec[0];
+    guess = s.spec[1];
+  }
   if (cut) {
-    ct = tie_group<DT>(s, h, k_lo, dv, m);
     const double kf = (ct.w > 0.0) ? floor((tau - ct.above) / ct.w) + 1.0 : (double)ct.n;
     n_keep = (int)fmax(1.0, fmin(kf, (double)ct.n));
     zp = ct.above + (double)n_keep * ct.w;
@@ -1346,9 +1366,13 @@ __device__ __forceinline__ bool resolve16(const Smem& s, int V, const Divider& d
   TieGroup dt = ct;
   int n_avail = n_keep;
   if (!cut || t < ct.above) {
-    const uint32_t dlo = cut ? ct.hi + 1u : k_lo;
-    if (!find_by_mass<DT>(s, dlo, t, dv, m, h)) return false;
-    dt = tie_group<DT>(s, h, dlo, dv, m);
+    if (cut && have_guess && guess.lo > ct.hi && t >= guess.above && t < guess.above + (double)guess.n * guess.w) {
+      dt = guess;
+    } else {
+      const uint32_t dlo = cut ? ct.hi + 1u : k_lo;
+      if (!find_by_mass<DT>(s, dlo, t, dv, m, h)) return false;
+      dt = tie_group<DT>(s, h, dlo, dv, m);
+    }
     n_avail = (int)dt.n;
   }
   st.sel_lo = dt.lo;
