@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="mixed256_llama3_bf16",
                     choices=["mixed256_llama3_bf16", "greedy512_quantized", "nucleus1024_qwen_fp32",
-                             "steps8_smollm_mixed"])
+                             "steps8_smollm_mixed", "engine_step_smollm2"])
     ap.add_argument("--copies", type=int, default=0, help="logits copies to rotate over (default: > 256 MB)")
     ap.add_argument("--cpu-steps", type=int, default=5, help="CPU baseline steps (median)")
     ap.add_argument("--cpu-rows", type=int, default=0, help="CPU baseline rows per step (0: all)")
@@ -112,12 +112,57 @@ def cpu_baseline(w, steps: int, rows: int):
     }
 
 
+def engine_step(args):
+    """The end-to-end engine step (smollm2-135m-random, 64 requests x 128 prompt + 128
+    output tokens, half greedy, half top-k=50 / top-p=0.9): decode throughput and the
+    sampler's share of the step, with the batched call and with one call per row."""
+    import torch
+
+    from pagedbatch_amd import engine_step as es
+
+    shape = es.ModelShape()
+    kw = dict(num_seqs=64, prompt_len=128, output_len=128, block_size=16, device="cuda")
+    print("[bench] engine step: warm-up", file=sys.stderr, flush=True)
+    es.run(shape, **{**kw, "output_len": 4})
+    print("[bench] engine step: batched sampling", file=sys.stderr, flush=True)
+    tb, out_b = es.run(shape, **kw)
+    print("[bench] engine step: one sampling call per row", file=sys.stderr, flush=True)
+    tr, out_r = es.run(shape, **kw, per_row=True)
+    same = out_b == out_r
+
+    def split(t):
+        fwd, smp = t.forward_s[1:], t.sample_s[1:]  # decode steps (step 0 is the prefill)
+        n = len(fwd)
+        return {"decode_steps": n, "forward_ms": round(1e3 * sum(fwd) / n, 4),
+                "sample_ms": round(1e3 * sum(smp) / n, 4),
+                "sample_share": round(sum(smp) / (sum(fwd) + sum(smp)), 4),
+                "prefill_forward_ms": round(1e3 * t.forward_s[0], 3), "prefill_sample_ms": round(1e3 * t.sample_s[0], 4)}
+
+    b, r = split(tb), split(tr)
+    step_ms = b["forward_ms"] + b["sample_ms"]
+    line = {
+        "metric": "engine decode tokens/s (smollm2-135m-random bf16, 64 requests, 128 prompt + 128 output tokens)",
+        "value": round(64 / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": b["decode_steps"],
+        "warmup": 1, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights, random prompt ids)",
+        "config": {"workload": "engine_step_smollm2", "requests": 64, "prompt_len": 128, "output_len": 128,
+                   "block_size": 16, "mix": "half greedy, half top_k=50 top_p=0.9 T=1.0"},
+        "batched_sampling": b, "per_row_sampling": r, "same_tokens_batched_vs_per_row": same,
+        "torch": torch.__version__,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build samples on a single device and has no "
               f"multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "engine_step_smollm2":
+        engine_step(args)
+        return
 
     import numpy as np
     import torch

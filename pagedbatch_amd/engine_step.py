@@ -1,0 +1,224 @@
+"""A minimal batched decode loop around the sampler: the engine step of pagedbatch with the
+per-row sampling loop hoisted into one ``sample()`` call per step.
+
+It exists to measure the sampler inside an engine step (the reference's end-to-end
+configuration: smollm2-135m-shaped random model, block size 16, 64 requests of 128
+prompt tokens and 128 output tokens, half greedy and half top-k=50 / top-p=0.9). The model
+is plain PyTorch and follows the Llama layout of pagedbatch/model.py:150-296 (RMSNorm,
+rotate-half RoPE, grouped-query attention over a paged KV cache written through a slot
+mapping, SwiGLU MLP, tied LM head, N(0, 0.02) initialisation); the sampling is this
+package's kernel. What the engine does per step (pagedbatch/engine.py:104-139): one forward
+over the scheduled tokens, logits of each sequence's last token, then one token per
+sequence, here from a single batched call (the hoist of engine.py:133-139).
+
+Out of scope: scheduling, preemption, chunked prefill, stop strings and the server; every
+request here runs from prefill to its last token in lockstep.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .config import SamplingParams
+from .sampling import sample
+
+
+@dataclass
+class ModelShape:
+    """pagedbatch/config.py:60-75 (the shape of HuggingFaceTB/SmolLM2-135M)."""
+
+    vocab_size: int = 49152
+    hidden_size: int = 576
+    intermediate_size: int = 1536
+    num_layers: int = 30
+    num_heads: int = 9
+    num_kv_heads: int = 3
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 100000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads
+
+    @classmethod
+    def tiny(cls) -> "ModelShape":
+        return cls(vocab_size=512, hidden_size=64, intermediate_size=128, num_layers=2, num_heads=4, num_kv_heads=2)
+
+
+class Model:
+    """Weights as plain tensors; forward over a flat token batch with a paged KV cache."""
+
+    def __init__(self, shape: ModelShape, device: torch.device, dtype=torch.bfloat16, seed: int = 0,
+                 max_positions: int = 4096):
+        self.shape = shape
+        g = torch.Generator().manual_seed(seed)
+        H, I, D = shape.hidden_size, shape.intermediate_size, shape.head_dim
+
+        def w(out_dim, in_dim):
+            # [out, in] drawn like nn.Linear's weight, stored transposed ([in, out], contiguous)
+            # so that every product is x @ W with no transposed operand
+            return (torch.randn(out_dim, in_dim, generator=g) * 0.02).t().contiguous().to(device=device, dtype=dtype)
+
+        embed = (torch.randn(shape.vocab_size, H, generator=g) * 0.02).to(device=device, dtype=dtype)
+        self.embed = embed
+        self.head = embed.t().contiguous()  # the tied LM head, [H, vocab]
+        self.layers = []
+        for _ in range(shape.num_layers):
+            self.layers.append({
+                "qkv": w((shape.num_heads + 2 * shape.num_kv_heads) * D, H),
+                "o": w(H, shape.num_heads * D),
+                "gate_up": w(2 * I, H),
+                "down": w(H, I),
+                "ln1": torch.ones(H, device=device, dtype=dtype),
+                "ln2": torch.ones(H, device=device, dtype=dtype),
+            })
+        self.norm = torch.ones(H, device=device, dtype=dtype)
+        inv = 1.0 / (shape.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        f = torch.outer(torch.arange(max_positions, dtype=torch.float32), inv)
+        emb = torch.cat([f, f], dim=-1)
+        self.cos = emb.cos().to(device)
+        self.sin = emb.sin().to(device)
+
+    def _rms(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        x32 = x.float()
+        return w * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + self.shape.rms_norm_eps)).to(x.dtype)
+
+    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        # x [T, heads, D] in fp32; rotate-half convention
+        cos, sin = self.cos[pos].unsqueeze(1), self.sin[pos].unsqueeze(1)
+        half = x.shape[-1] // 2
+        rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+        return x * cos + rot * sin
+
+    @torch.no_grad()
+    def forward(self, tokens: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor, seq_slots: torch.Tensor,
+                q_len: int, cache: "PagedKV") -> torch.Tensor:
+        """``tokens``/``pos``/``slots``: [B * q_len] (sequence-major); ``seq_slots``: [B, L] the
+        cache slots of each sequence's whole context, new tokens last. Returns [B, vocab]
+        logits of each sequence's last token."""
+        s = self.shape
+        D, Hq, Hkv = s.head_dim, s.num_heads, s.num_kv_heads
+        B, L = seq_slots.shape
+        x = self.embed[tokens]
+        scale = 1.0 / math.sqrt(D)
+        causal = None
+        if q_len > 1:
+            qi = torch.arange(L - q_len, L, device=x.device).view(q_len, 1)
+            causal = torch.arange(L, device=x.device).view(1, L) > qi  # True = masked
+        for li, p in enumerate(self.layers):
+            h = self._rms(x, p["ln1"])
+            qkv = h @ p["qkv"]
+            q = qkv[:, : Hq * D].view(-1, Hq, D).float()
+            k = qkv[:, Hq * D : (Hq + Hkv) * D].view(-1, Hkv, D).float()
+            v = qkv[:, (Hq + Hkv) * D :].view(-1, Hkv, D)
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            cache.k[li].index_copy_(0, slots, k.to(cache.k[li].dtype))
+            cache.v[li].index_copy_(0, slots, v)
+            # attention in fp32 with contiguous operands: [B, Hkv, rep, q_len, D] x [B, Hkv, D, L]
+            keys = cache.k[li][seq_slots].float().permute(0, 2, 3, 1).contiguous()  # [B, Hkv, D, L]
+            vals = cache.v[li][seq_slots].float().permute(0, 2, 1, 3).contiguous()  # [B, Hkv, L, D]
+            qh = q.view(B, q_len, Hkv, Hq // Hkv, D).permute(0, 2, 3, 1, 4).reshape(B, Hkv, -1, D).contiguous()
+            att = torch.matmul(qh, keys) * scale  # [B, Hkv, rep * q_len, L]
+            if causal is not None:
+                att = att.view(B, Hkv, Hq // Hkv, q_len, L).masked_fill(causal, float("-inf")).view(B, Hkv, -1, L)
+            o = torch.matmul(torch.softmax(att, dim=-1), vals)  # [B, Hkv, rep * q_len, D]
+            o = o.view(B, Hkv, Hq // Hkv, q_len, D).permute(0, 3, 1, 2, 4).reshape(B * q_len, Hq * D)
+            x = x + o.to(x.dtype) @ p["o"]
+            h = self._rms(x, p["ln2"])
+            gu = h @ p["gate_up"]
+            x = x + (F.silu(gu[:, : s.intermediate_size]) * gu[:, s.intermediate_size :]) @ p["down"]
+        last = self._rms(x.view(B, q_len, -1)[:, -1], self.norm)
+        return last @ self.head
+
+
+class PagedKV:
+    """Per-layer K/V slot pools ([slots, kv_heads, head_dim]) in blocks of ``block_size``
+    slots; each sequence owns whole blocks through its block table (block_manager.py:88-91:
+    slot = block * block_size + offset)."""
+
+    def __init__(self, shape: ModelShape, num_seqs: int, max_len: int, block_size: int, device, dtype):
+        self.block_size = block_size
+        blocks_per_seq = (max_len + block_size - 1) // block_size
+        nslots = num_seqs * blocks_per_seq * block_size
+        self.k = [torch.empty(nslots, shape.num_kv_heads, shape.head_dim, device=device, dtype=dtype)
+                  for _ in range(shape.num_layers)]
+        self.v = [torch.empty_like(t) for t in self.k]
+        # block tables: sequence i holds blocks i, i + num_seqs, i + 2 num_seqs, ... (interleaved,
+        # so that a sequence's blocks are not contiguous in the pool)
+        self.block_table = torch.arange(blocks_per_seq, device=device).view(1, -1) * num_seqs + \
+            torch.arange(num_seqs, device=device).view(-1, 1)
+
+    def slots(self, seq: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """Slots of positions ``pos`` of sequences ``seq`` (broadcast)."""
+        blk = self.block_table[seq, pos // self.block_size]
+        return blk * self.block_size + pos % self.block_size
+
+
+@dataclass
+class StepTimes:
+    """Per-step wall times (s): the forward (logits ready on the device) and the sampling
+    call (params, uniforms, launch, kernel, token copy back). Step 0 is the prefill."""
+
+    forward_s: list = None
+    sample_s: list = None
+    tokens_per_step: int = 0
+
+    def __post_init__(self):
+        self.forward_s = []
+        self.sample_s = []
+
+
+def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len: int = 128, block_size: int = 16,
+        device: str | torch.device = "cuda", seed: int = 0, per_row: bool = False) -> tuple[StepTimes, list[list[int]]]:
+    """Prefill every prompt, then decode in lockstep until each request has ``output_len``
+    tokens. Half the requests are greedy, half top-k=50 / top-p=0.9 at temperature 1.0; the
+    unseeded ones share one engine generator (engine.py:58). ``per_row`` samples with one
+    ``sample_token`` call per sequence (the reference loop, unhoisted) instead of one batched
+    ``sample``. Returns the time split and the generated tokens."""
+    device = torch.device(device)
+    model = Model(shape, device, seed=seed)
+    cache = PagedKV(shape, num_seqs, prompt_len + output_len, block_size, device, torch.bfloat16)
+    g = torch.Generator().manual_seed(seed + 1)
+    prompts = torch.randint(3, shape.vocab_size, (num_seqs, prompt_len), generator=g)
+    params = [SamplingParams(temperature=0.0) if i % 2 == 0 else SamplingParams(temperature=1.0, top_k=50, top_p=0.9)
+              for i in range(num_seqs)]
+    engine_gen = torch.Generator().manual_seed(seed + 2)
+    gens = [engine_gen] * num_seqs
+    seq = torch.arange(num_seqs, device=device)
+    out: list[list[int]] = [[] for _ in range(num_seqs)]
+    times = StepTimes(tokens_per_step=num_seqs)
+
+    def step(tokens: torch.Tensor, start: int, q_len: int) -> list[int]:
+        pos = torch.arange(start, start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
+        slots = cache.slots(seq.view(-1, 1), pos).reshape(-1)
+        ctx = torch.arange(start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
+        seq_slots = cache.slots(seq.view(-1, 1), ctx)
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        logits = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache)
+        torch.cuda.synchronize(device)
+        t1 = time.perf_counter()
+        if per_row:
+            from .sampling import sample_token
+            toks = [sample_token(logits[i], params[i], gens[i]) for i in range(num_seqs)]
+        else:
+            toks = sample(logits, params, gens)
+        t2 = time.perf_counter()
+        times.forward_s.append(t1 - t0)
+        times.sample_s.append(t2 - t1)
+        return toks
+
+    toks = step(prompts.to(device), 0, prompt_len)
+    for i, t in enumerate(toks):
+        out[i].append(t)
+    for n in range(1, output_len):
+        cur = torch.tensor([o[-1] for o in out], device=device).view(-1, 1)
+        toks = step(cur, prompt_len + n - 1, 1)
+        for i, t in enumerate(toks):
+            out[i].append(t)
+    return times, out

@@ -170,13 +170,31 @@ def _raise_for_status(status: np.ndarray) -> None:
 
 
 def draw_uniforms(params: Sequence, generators: Sequence[torch.Generator]) -> list[float]:
-    """One ``torch.rand`` draw per stochastic row, in row order; greedy rows draw nothing."""
-    out = []
-    for sp, g in zip(params, generators):
-        if sp.temperature == 0:
-            out.append(0.0)
-        else:
-            out.append(float(torch.rand((), generator=g, device=g.device)))
+    """One ``torch.rand`` draw per stochastic row, in row order; greedy rows draw nothing.
+
+    Consecutive stochastic rows that share a generator (the engine's shared generator for
+    unseeded requests, engine.py:58) take their draws from one ``torch.rand(n)`` call: torch
+    fills it with the same numbers, in the same order, as n scalar draws, and leaves the
+    generator in the same state.
+    """
+    out = [0.0] * len(params)
+    i, n = 0, len(params)
+    while i < n:
+        if params[i].temperature == 0:
+            i += 1
+            continue
+        g = generators[i]
+        j = i + 1
+        idx = [i]
+        # extend the run over greedy rows (which draw nothing) while the generator repeats
+        while j < n and (params[j].temperature == 0 or generators[j] is g):
+            if params[j].temperature != 0:
+                idx.append(j)
+            j += 1
+        vals = torch.rand(len(idx), generator=g, device=g.device).tolist()
+        for k, v in zip(idx, vals):
+            out[k] = float(v)
+        i = j
     return out
 
 

@@ -65,6 +65,25 @@ def test_draw_uniforms_consumes_generators_like_the_reference():
     assert float(torch.rand((), generator=shared)) == float(torch.rand((), generator=ref))
 
 
+def test_draw_uniforms_mixed_generators_match_scalar_draws():
+    """Runs of rows sharing a generator are drawn in one call; the numbers and the final
+    generator states equal one scalar torch.rand per stochastic row in row order."""
+    def make():
+        shared = torch.Generator().manual_seed(7)
+        seeded = [torch.Generator().manual_seed(100 + i) for i in range(3)]
+        gens = [shared, shared, seeded[0], shared, shared, shared, seeded[1], seeded[1], shared, seeded[2]] * 3
+        return shared, seeded, gens
+    temps = [1.0, 0.0, 0.7, 1.0, 0.0, 1.3, 1.0, 1.0, 0.0, 0.9] * 3
+    params = [SamplingParams(temperature=t) for t in temps]
+    shared, seeded, gens = make()
+    us = smp.draw_uniforms(params, gens)
+    rshared, rseeded, rgens = make()
+    want = [float(torch.rand((), generator=g)) if t != 0 else 0.0 for t, g in zip(temps, rgens)]
+    assert us == want
+    for a, b in zip([shared] + seeded, [rshared] + rseeded):
+        assert float(torch.rand((), generator=a)) == float(torch.rand((), generator=b))
+
+
 def test_no_cpu_path():
     x = torch.randn(2, 100)
     with pytest.raises(ValueError, match="no CPU path"):
@@ -167,3 +186,18 @@ def test_debug_outputs_need_info():
     rc = lib.pbs_sample_debug(1 << 20, _lib.DTYPE_F32, 1, 1, 10, 10, None, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
                               1 << 20, 1 << 20, 1 << 20, None, None, None, 0, None)
     assert rc == _lib.ERR_INVALID_ARGUMENT and "out_info" in _lib.last_error(lib)
+
+
+def test_paged_kv_slots_are_distinct_and_blocked():
+    """Block tables give every (sequence, position) its own slot, block_size consecutive
+    positions per block (block_manager.py:88-91)."""
+    from pagedbatch_amd.engine_step import ModelShape, PagedKV
+
+    kv = PagedKV(ModelShape.tiny(), num_seqs=5, max_len=37, block_size=8, device="cpu", dtype=torch.float32)
+    seq = torch.arange(5).view(-1, 1)
+    pos = torch.arange(37).view(1, -1).expand(5, -1)
+    s = kv.slots(seq, pos)
+    assert s.unique().numel() == 5 * 37
+    assert int(s.max()) < kv.k[0].shape[0]
+    # within a block the slots are consecutive
+    assert torch.equal(s[:, 1:8] - s[:, :7], torch.ones(5, 7, dtype=s.dtype))
