@@ -188,11 +188,29 @@ def test_values_colliding_after_division(dev, dtype):
     run_case(dev, f"collide_{DT_NAME[dtype]}", logits, T, K, P, U)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fp32_window_paths(dev):
+    """fp32 rows through each way the window path resolves: top-k within the top 4096 (one
+    list), large top-k with and without top-p (the k-th element's bin gathered with the
+    cutoff and draw windows), temperature 1 and not 1 (the division), and tie-heavy rows
+    whose windows hold more elements than the LDS list (the general path)."""
+    g = torch.Generator().manual_seed(24)
+    V = 131072
+    x = torch.randn(8, V, generator=g) * 0.5
+    x[6:] = torch.round(x[6:] * 4) / 4  # few distinct values, tens of thousands of elements each
+    T = [1.0, 0.8, 1.0, 1.3, 0.6, 1.0, 1.0, 0.9]
+    K = [20, 3000, 60000, 90000, 0, 0, 0, 500]
+    P = [0.9, 0.95, 0.8, 1.0, 0.95, 1.0, 0.9, 0.97]
+    U = [float(v) for v in torch.rand(8, generator=g)]
+    run_case(dev, "fp32_window_paths", x, T, K, P, U, want_probs=False, info_only=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_register_row_sizes(dev, dtype):
     """Vocab sizes that land on each register-row width (and just past the largest)."""
     g = torch.Generator().manual_seed(23)
-    for V in (4096, 8192, 12288, 24576, 49152, 128256, 131072, 151936):
+    sizes = (2048, 4096, 8192, 16384, 24576, 32768, 49152, 65536, 151936) if dtype == torch.float32 else \
+        (4096, 8192, 12288, 24576, 49152, 128256, 131072, 151936)
+    for V in sizes:
         x = (torch.randn(8, V, generator=g) * 2.0).to(dtype)
         T = [0.0, 0.9, 1.0, 1.2] * 2
         K = [0, 40, 0, V // 3, 1, 0, 7, 0]
