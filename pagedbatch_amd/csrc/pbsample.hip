@@ -1277,14 +1277,72 @@ __device__ __forceinline__ TieGroup tie_group(const Smem& s, const BinHit& h, ui
   return t;
 }
 
+// The k-th largest element by counts alone (before any mass is known): its ord, the ord
+// range of its tie group, the group's count and the count above it. Wave-local: the
+// counts above each group come from a wave scan of the group counts.
+struct KthCount {
+  uint32_t o, lo, hi, n, n_above;
+  bool ok;
+};
+
+// elements with ord >= t (whole wave, from the group counts)
+__device__ __forceinline__ uint32_t count_ge_local(const Smem& s, uint32_t t) {
+  if (t > 0xffffu) return 0u;
+  const uint32_t g = t >> 8;
+  const int l = lane_id();
+  uint32_t c = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c += (4u * (uint32_t)l + (uint32_t)i > g) ? s.gcount[4 * l + i] : 0u;
+  return wsum_u32(c) + count_above_in_group(s, g, t - 1u);
+}
+
+template <int DT>
+__device__ __forceinline__ KthCount kth_by_count(const Smem& s, uint32_t need, const Divider& dv) {
+  const int l = lane_id();
+  KthCount r = {};
+  // lane l holds groups 255-4l .. 252-4l (descending); the scan gives the count above each
+  uint32_t c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = s.gcount[255 - 4 * l - i];
+  const uint32_t ct = (c[0] + c[1]) + (c[2] + c[3]);
+  uint32_t run = wscan_u32(ct) - ct;
+  int fi = -1;
+  uint32_t fa = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (fi < 0 && c[i] && run + c[i] >= need) {
+      fi = i;
+      fa = run;
+    }
+    run += c[i];
+  }
+  const uint64_t hit = ballot(fi >= 0);
+  if (!hit) return r;
+  const int L = first_lane(hit);
+  const uint32_t g = 255u - 4u * (uint32_t)L - bcast_u32((uint32_t)fi, L);
+  const uint32_t above_g = bcast_u32(fa, L);
+  uint32_t cnt, ca;
+  bins_count(s, g, need - above_g, r.o, cnt, ca);
+  tie_range16<DT>(r.o, dv, r.lo, r.hi);
+  if (r.lo == r.o && r.hi == r.o) {
+    r.n = cnt;
+    r.n_above = above_g + ca;
+  } else {
+    r.n_above = count_ge_local(s, r.hi + 1u);
+    r.n = count_ge_local(s, r.lo) - r.n_above;
+  }
+  r.ok = true;
+  return r;
+}
+
 // Top-k threshold, top-p cutoff and draw position from the histogram summaries. Every
 // wave runs it and ends with the same RowState. The searches are wave-local, except that
 // with top-p the cutoff and a guessed draw run side by side on the two halves of the
 // waves (one barrier). Returns false if a u16 counter wrapped (one value more than 65535
 // times): the caller then takes the general path.
 template <int DT>
-__device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int kk, float p, float u, float m,
-                                          bool want_info, RowState& st) {
+__device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int kk, const KthCount& kc, float p,
+                                          float u, float m, bool want_info, RowState& st) {
   const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
   if (total_cnt != (uint32_t)V) return false;
   st = RowState{};
@@ -1301,10 +1359,17 @@ __device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int
   TieGroup kt = {};
   const bool topk = kk > 0 && kk < V;
   if (topk) {
-    if (!find_by_count<DT>(s, (uint32_t)kk, dv, m, h)) return false;
-    kt = tie_group<DT>(s, h, 0u, dv, m);
+    // found by counts before the masses (kth_by_count); Z_K = the mass above its tie
+    // group plus the group's count times its weight
+    kt.lo = kc.lo;
+    kt.hi = kc.hi;
+    kt.n = kc.n;
+    kt.n_above = kc.n_above;
+    uint32_t c_ge;
+    count_mass_ge<DT>(s, kc.hi + 1u, dv, m, c_ge, kt.above);
+    kt.w = weight16<DT>(kc.o, dv, m);
     k_lo = kt.lo;
-    st.x_kth = scaled16<DT>(h.o, dv);
+    st.x_kth = scaled16<DT>(kc.o, dv);
     zk = kt.above + (double)kt.n * kt.w;
     nk = kt.n_above + kt.n;
   }
@@ -1506,12 +1571,23 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
     return true;
   }
 
-  // group masses: the non-empty groups, ranked and dealt round-robin to the waves; lane l
-  // weighs ords 4l .. 4l+3 of the group
+  // top-k (sampling.py:15-17): the k-th element by counts; only its tie group and the
+  // groups above it (K) need masses
+  const bool topk = kk > 0 && kk < V;
+  KthCount kc = {};
+  uint32_t glo = 0u;
+  if (topk) {
+    kc = kth_by_count<DT>(s, (uint32_t)kk, dv);
+    if (!kc.ok) return false;
+    glo = kc.lo >> 8;
+  }
+
+  // group masses: the non-empty groups from glo up, ranked and dealt round-robin to the
+  // waves; lane l weighs ords 4l .. 4l+3 of the group (the others get mass 0)
   {
     uint32_t ne = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ne |= (s.gcount[4 * l + i] != 0u ? 1u : 0u) << i;
+    for (int i = 0; i < 4; ++i) ne |= (s.gcount[4 * l + i] != 0u && 4u * (uint32_t)l + (uint32_t)i >= glo ? 1u : 0u) << i;
     if (wv == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -1581,7 +1657,7 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   }
   __syncthreads();
   RowState st;
-  if (!resolve16<DT>(s, V, dv, kk, p, u, m, a.out_info != nullptr, st)) return false;  // a counter wrapped
+  if (!resolve16<DT>(s, V, dv, kk, kc, p, u, m, a.out_info != nullptr, st)) return false;  // a counter wrapped
 
   // which of the tied tokens: the sel_rank-th lowest index with ord in [sel_lo, sel_hi]
   const int tok = select_tied16<DT>(src, s, st.sel_lo, st.sel_hi, st.sel_rank);
