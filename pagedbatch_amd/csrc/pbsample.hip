@@ -42,7 +42,7 @@ constexpr int NBUCKET = 256;       // fp32 rows: buckets per level of a list sea
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Workgroup barrier that orders LDS traffic only. Unlike __syncthreads() it does not make
 // the wave wait for its outstanding global loads, so row chunks keep streaming in while
@@ -316,15 +316,24 @@ struct Divider {
       ehi = 0;
     }
   }
+  // the FMA sequence alone: exact for a with biased exponent in [elo, ehi]
+  __device__ __forceinline__ float fma_seq(float a) const {
+    float q = a * r;
+    float res = fmaf(-q, T, a);
+    q = fmaf(res, r, q);
+    res = fmaf(-q, T, a);
+    return fmaf(res, r, q);
+  }
+  __device__ __forceinline__ bool safe_exp(int e) const { return e >= elo && e <= ehi; }
+  // operator() behind one wave-uniform branch: the FMA sequence when every active lane
+  // may take it (latency-bound code, where per-lane branches cost more than the division)
+  __device__ __forceinline__ float uniform(float a) const {
+    if (__all(safe_exp((int)((__float_as_uint(a) >> 23) & 0xff)))) return fma_seq(a);
+    return (*this)(a);
+  }
   __device__ __forceinline__ float operator()(float a) const {
     const int e = (int)((__float_as_uint(a) >> 23) & 0xff);
-    if (e >= elo && e <= ehi) {
-      float q = a * r;
-      float res = fmaf(-q, T, a);
-      q = fmaf(res, r, q);
-      res = fmaf(-q, T, a);
-      return fmaf(res, r, q);
-    }
+    if (e >= elo && e <= ehi) return fma_seq(a);
     if ((__float_as_uint(a) & 0x7fffffffu) == 0u) return a * r;  // +-0
     if (e == 255) return a * r;                                   // +-inf, NaN
     return a / T;
@@ -412,6 +421,8 @@ struct __align__(16) Smem {
   int sel_jstar, sel_rank, sel_index;
   TieGroup spec[2];              // 16-bit rows: cutoff and guessed draw, searched side by side
   int spec_ok[2];
+  uint32_t res_lo, res_hi;       // 16-bit rows: the drawn tie group (ords) and the rank in it
+  int res_rank, res_ok;
   RowState st;
 };
 
@@ -818,20 +829,29 @@ __device__ __forceinline__ uint32_t wave_totals16(const uint32_t (&P)[16]) {
   return t;
 }
 
-// r[j] for a run-time (wave-uniform) j < N by a chain of selects: one vector live, not N.
-// Each vector first passes through an empty asm statement: as plain loads from the row
-// array the selects would be folded into one indexed load, moving the row to scratch.
+// r[j] for a run-time, wave-uniform j < N: a switch on j (scalar compares and branches,
+// only the taken case moves a vector). The empty asm statement in each case keeps the
+// cases apart: merged into selects, or into one indexed load from the row array, they
+// would cost N times the moves or move the row to scratch.
 template <int N>
 __device__ __forceinline__ u4 pick_chunk(const u4 (&r)[N], int j) {
   u4 q = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    uint32_t a = r[i].x, b = r[i].y, c = r[i].z, d = r[i].w;
-    asm("" : "+v"(a));
-    asm("" : "+v"(b));
-    asm("" : "+v"(c));
-    asm("" : "+v"(d));
-    if (i == j) q = (u4){a, b, c, d};
+  switch (j) {
+#define PBS_PICK(i)                                                  \
+  case i:                                                            \
+    if constexpr (i < N) {                                           \
+      uint32_t a = r[i].x, b = r[i].y, c = r[i].z, d = r[i].w;       \
+      asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));         \
+      q = (u4){a, b, c, d};                                          \
+    }                                                                \
+    break;
+    PBS_PICK(0) PBS_PICK(1) PBS_PICK(2) PBS_PICK(3) PBS_PICK(4) PBS_PICK(5) PBS_PICK(6) PBS_PICK(7)
+    PBS_PICK(8) PBS_PICK(9) PBS_PICK(10) PBS_PICK(11) PBS_PICK(12) PBS_PICK(13) PBS_PICK(14) PBS_PICK(15)
+    PBS_PICK(16) PBS_PICK(17) PBS_PICK(18) PBS_PICK(19) PBS_PICK(20) PBS_PICK(21) PBS_PICK(22) PBS_PICK(23)
+    PBS_PICK(24) PBS_PICK(25) PBS_PICK(26) PBS_PICK(27) PBS_PICK(28) PBS_PICK(29) PBS_PICK(30) PBS_PICK(31)
+#undef PBS_PICK
+    default:
+      break;
   }
   return q;
 }
@@ -848,48 +868,47 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
     // min(x, 1) as two compares and two selects
     uint32_t one2 = 0x00010001u;
     asm("" : "+v"(one2));
-    // per-lane misses of the valid vectors, chunks 2r and 2r + 1 packed in P[r]
+    // per-lane misses of every vector, chunks 2r and 2r + 1 packed in P[r]; vectors past
+    // the row end hold zeros (the loads' range check) and are corrected for below
     uint32_t P[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) P[r] = 0u;
     if (span == 0u) {
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const uint32_t c = lane_misses16<ORD, true>(src.r[j], lo2, span2, one2);
-        P[j >> 1] |= (j * NT + (int)threadIdx.x < src.nvec ? c : 0u) << (16 * (j & 1));
-      }
+      for (int j = 0; j < NCH; ++j) P[j >> 1] |= lane_misses16<ORD, true>(src.r[j], lo2, span2, one2) << (16 * (j & 1));
     } else {
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const uint32_t c = lane_misses16<ORD, false>(src.r[j], lo2, span2, one2);
-        P[j >> 1] |= (j * NT + (int)threadIdx.x < src.nvec ? c : 0u) << (16 * (j & 1));
-      }
+      for (int j = 0; j < NCH; ++j) P[j >> 1] |= lane_misses16<ORD, false>(src.r[j], lo2, span2, one2) << (16 * (j & 1));
     }
     const uint32_t t = wave_totals16(P);
     if ((l & 3) == 0) {
-      // matches = 8 per valid lane of the (chunk, wave) minus its misses
+      // matches = 8 per valid lane of the (chunk, wave) minus the valid lanes' misses; a
+      // lane past the row end counted 8 misses unless the key of 0 lies in the range
+      const uint32_t zero_in = (((key16x2<ORD>(0u) & 0xffffu) - lo) & 0xffffu) <= span ? 1u : 0u;
       const int r = l >> 2;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int j = 2 * r + h;
         if (j < NCH) {
           const int first = j * NT + w * 64;
-          const int nlanes = min(64, max(0, src.nvec - first));
-          s.hist[j * NWAVE + w] = 8u * (uint32_t)nlanes - ((t >> (16 * h)) & 0xffffu);
+          const uint32_t nlanes = (uint32_t)min(64, max(0, src.nvec - first));
+          const uint32_t miss_all = (t >> (16 * h)) & 0xffffu;
+          s.hist[j * NWAVE + w] = 8u * nlanes - miss_all + 8u * (64u - nlanes) * (1u - zero_in);
         }
       }
     }
   }
   __syncthreads();
-  if (w == 0) {
-    // positions p = j*NWAVE + wave are in index order; lane l holds p = 4l .. 4l+3
+  // every wave scans the totals (positions p = j*NWAVE + wave are in index order; lane l
+  // holds p = 4l .. 4l+3), so no second barrier hands the answer around
+  int pos = -1, rr = 0;
+  {
     uint32_t c[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) c[i] = (4 * l + i < NCH * NWAVE) ? s.hist[4 * l + i] : 0u;
     const uint32_t tot = c[0] + c[1] + c[2] + c[3];
     const uint32_t incl = wscan_u32(tot);
     const uint64_t hit = ballot(incl > (uint32_t)rank);
-    int pos = -1, rr = 0;
     if (hit) {
       const int L = first_lane(hit);
       uint32_t run = incl - tot;
@@ -907,16 +926,11 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
       pos = (int)bcast_u32((uint32_t)(4 * l + fi), L);
       rr = (int)bcast_u32((uint32_t)fr, L);
     }
-    if (l == 0) {
-      s.sel_jstar = pos;
-      s.sel_rank = rr;
-      s.sel_index = -1;
-    }
   }
-  __syncthreads();
-  const int pos = s.sel_jstar;
-  if (pos >= 0) {
-    const int jstar = pos / NWAVE, wstar = pos % NWAVE, rr = s.sel_rank;
+  if (pos < 0) {
+    if (threadIdx.x == 0) s.sel_index = -1;
+  } else {
+    const int jstar = pos / NWAVE, wstar = pos % NWAVE;
     if (w == wstar) {
       const u4 q = pick_chunk<NCH>(src.r, jstar);
       const uint32_t bits = (jstar * NT + (int)threadIdx.x < src.nvec) ? match_bits16<ORD>(q, lo2, span) : 0u;
@@ -1017,13 +1031,22 @@ __device__ __forceinline__ void hist_add_one(Smem& s, uint32_t raw) {
 
 template <int DT>
 __device__ __forceinline__ float scaled16(uint32_t o, const Divider& dv) {
-  return dv(raw_to_float<DT>(raw_of_ord16(o)));
+  return dv.uniform(raw_to_float<DT>(raw_of_ord16(o)));
 }
 // softmax weight of one distinct value relative to the row maximum m, in fp64 from the
 // exact fp32 scaled value (pagedbatch takes softmax of the fp32 scaled row, sampling.py:26)
 template <int DT>
 __device__ __forceinline__ double weight16(uint32_t o, const Divider& dv, float m) {
   return weight_f(scaled16<DT>(o, dv), m);
+}
+// whether every value of group g divides by the FMA sequence: the group's smallest and
+// largest magnitudes (raw low byte 0x00 and 0xff) bound its exponents
+template <int DT>
+__device__ __forceinline__ bool group_fma16(uint32_t g, const Divider& dv) {
+  const uint32_t rb = raw_of_ord16(g << 8) & 0xff00u;
+  const int e0 = (int)((__float_as_uint(raw_to_float<DT>(rb)) >> 23) & 0xff);
+  const int e1 = (int)((__float_as_uint(raw_to_float<DT>(rb | 0xffu)) >> 23) & 0xff);
+  return dv.safe_exp(e0) && dv.safe_exp(e1);
 }
 template <int DT>
 __device__ __forceinline__ float weight16f(uint32_t o, const Divider& dv, float m) {
@@ -1162,6 +1185,17 @@ __device__ __forceinline__ void mass_above_in_sub(const Smem& s, uint32_t g, uin
   const float part = c ? (float)c * weight16f<DT>(ol, dv, m) : 0.0f;
   mass = (double)bcast_f32(wscan_f32(part), 63);
   w = (double)weight16f<DT>(o, dv, m);
+}
+
+// mass of the elements with ord > o from the prefix tables: the groups above o's group,
+// the subgroups above its subgroup, and the ords above it in its subgroup (fp32 inside
+// the subgroup), the same tables the searches' cumulative masses come from
+template <int DT>
+__device__ __forceinline__ double mass_above16(const Smem& s, uint32_t o, const Divider& dv, float m) {
+  const uint32_t g = o >> 8, k = (o & 255u) >> 5;
+  double ma, w;
+  mass_above_in_sub<DT>(s, g, k, o, dv, m, ma, w);
+  return s.gabove_mass[g] + s.subabove[g * 8u + k] + ma;
 }
 
 // the need-th element (descending) over all ords
@@ -1341,64 +1375,68 @@ __device__ __forceinline__ KthCount kth_by_count(const Smem& s, uint32_t need, c
 // waves (one barrier). Returns false if a u16 counter wrapped (one value more than 65535
 // times): the caller then takes the general path.
 template <int DT>
-__device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int kk, const KthCount& kc, float p,
+__device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int kk, const KthCount& kc, float p,
                                           float u, float m, bool want_info, RowState& st) {
-  const uint32_t total_cnt = s.gabove_cnt[0] + s.gcount[0];
-  if (total_cnt != (uint32_t)V) return false;
+  // Wave 0 searches (and wave 1 beside it, for the guessed draw): the other waves wait at
+  // the barriers instead of competing for their SIMDs' issue slots with copies of the same
+  // work (waves w and w + 4 share a SIMD). Wave 0 leaves the selection in s.res_*, which
+  // the caller reads after its next barrier; st is filled in wave 0 only.
+  const int wv = wave_id();
+  const bool side = p < 1.0f;
+  const bool topk = kk > 0 && kk < V;
+  BinHit h;
+  uint32_t k_lo = 0u;
+  uint32_t nk = (uint32_t)V;
+  double zk = 0.0;
+  TieGroup kt = {};
+  if (wv < (side ? 2 : 1)) {
+    zk = s.gabove_mass[0] + s.gmass[0];
+    // top-k (sampling.py:15-17): K = ords >= the tie group of the k-th largest element,
+    // found by counts before the masses (kth_by_count); Z_K = the mass above its tie
+    // group plus the group's count times its weight
+    if (topk) {
+      kt.lo = kc.lo;
+      kt.hi = kc.hi;
+      kt.n = kc.n;
+      kt.n_above = kc.n_above;
+      kt.above = mass_above16<DT>(s, kc.hi, dv, m);
+      kt.w = weight16<DT>(kc.o, dv, m);
+      k_lo = kt.lo;
+      zk = kt.above + (double)kt.n * kt.w;
+      nk = kt.n_above + kt.n;
+    }
+    // top-p (sampling.py:18-25): keep the shortest prefix whose exclusive mass is <= p * Z_K.
+    // Z_P lies in (tau, tau + one weight], so the draw's target u Z_P is close to u tau:
+    // wave 0 searches the cutoff while wave 1 searches the draw for u tau; the guess is
+    // kept below if u Z_P falls in the tie group it found.
+    if (side) {
+      const double tau = (double)p * zk;
+      const bool ok = find_by_mass<DT>(s, k_lo, wv == 1 ? (double)u * tau : tau, dv, m, h);
+      const TieGroup tg = ok ? tie_group<DT>(s, h, k_lo, dv, m) : TieGroup{};
+      if (lane_id() == 0) {
+        s.spec[wv] = tg;
+        s.spec_ok[wv] = ok ? 1 : 0;
+      }
+    }
+  }
+  if (side) __syncthreads();
+  if (wv != 0) return;
+
+  // a u16 counter wrapped if the group counts do not add up to V (the general path then
+  // takes the row)
+  bool ok = s.gabove_cnt[0] + s.gcount[0] == (uint32_t)V;
   st = RowState{};
   st.status = PBS_ROW_OK;
   st.m = m;
-  st.x_kth = -INFINITY;
-  const double z_all = s.gabove_mass[0] + s.gmass[0];
-  BinHit h;
-
-  // top-k (sampling.py:15-17): K = ords >= the tie group of the k-th largest element
-  uint32_t k_lo = 0u;
-  uint32_t nk = (uint32_t)V;
-  double zk = z_all;
-  TieGroup kt = {};
-  const bool topk = kk > 0 && kk < V;
-  if (topk) {
-    // found by counts before the masses (kth_by_count); Z_K = the mass above its tie
-    // group plus the group's count times its weight
-    kt.lo = kc.lo;
-    kt.hi = kc.hi;
-    kt.n = kc.n;
-    kt.n_above = kc.n_above;
-    uint32_t c_ge;
-    count_mass_ge<DT>(s, kc.hi + 1u, dv, m, c_ge, kt.above);
-    kt.w = weight16<DT>(kc.o, dv, m);
-    k_lo = kt.lo;
-    st.x_kth = scaled16<DT>(kc.o, dv);
-    zk = kt.above + (double)kt.n * kt.w;
-    nk = kt.n_above + kt.n;
-  }
+  st.x_kth = topk ? scaled16<DT>(kc.o, dv) : -INFINITY;
   st.zk = zk;
-
-  // top-p (sampling.py:18-25): keep the shortest prefix whose exclusive mass is <= p * Z_K.
-  // Z_P lies in (tau, tau + one weight], so the draw's target u Z_P is close to u tau: the
-  // first half of the waves searches the cutoff while the second half searches the draw
-  // for u tau; the guess is kept below if u Z_P falls in the tie group it found.
   TieGroup ct = kt;
   int n_keep;
   double zp;
   const double tau = (double)p * zk;
-  bool cut = false, have_guess = false;
-  TieGroup guess = {};
-  if (p < 1.0f) {
-    const bool second = wave_id() >= NWAVE / 2;
-    const bool ok = find_by_mass<DT>(s, k_lo, second ? (double)u * tau : tau, dv, m, h);
-    const TieGroup tg = ok ? tie_group<DT>(s, h, k_lo, dv, m) : TieGroup{};
-    if (lane_id() == 0 && (wave_id() == 0 || wave_id() == NWAVE / 2)) {
-      s.spec[second ? 1 : 0] = tg;
-      s.spec_ok[second ? 1 : 0] = ok ? 1 : 0;
-    }
-    __syncthreads();
-    cut = s.spec_ok[0] != 0;
-    have_guess = s.spec_ok[1] != 0;
-    if (cut) ct = s.spec[0];
-    guess = s.spec[1];
-  }
+  const bool cut = side && s.spec_ok[0] != 0;
+  const bool have_guess = side && s.spec_ok[1] != 0;
+  if (cut) ct = s.spec[0];
   if (cut) {
     const double kf = (ct.w > 0.0) ? floor((tau - ct.above) / ct.w) + 1.0 : (double)ct.n;
     n_keep = (int)fmax(1.0, fmin(kf, (double)ct.n));
@@ -1408,8 +1446,10 @@ __device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int
     // all of K is kept; the cutoff group is K's lowest value (for the diagnostics only: the
     // draw below searches all of K)
     if (!topk && want_info) {
-      if (!find_by_count<DT>(s, nk, dv, m, h)) return false;
-      ct = tie_group<DT>(s, h, 0u, dv, m);
+      if (find_by_count<DT>(s, nk, dv, m, h))
+        ct = tie_group<DT>(s, h, 0u, dv, m);
+      else
+        ok = false;
     }
     n_keep = (int)ct.n;
     zp = zk;
@@ -1430,13 +1470,16 @@ __device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int
   st.target = t;
   TieGroup dt = ct;
   int n_avail = n_keep;
-  if (!cut || t < ct.above) {
+  if (ok && (!cut || t < ct.above)) {
+    const TieGroup guess = s.spec[1];
     if (cut && have_guess && guess.lo > ct.hi && t >= guess.above && t < guess.above + (double)guess.n * guess.w) {
       dt = guess;
     } else {
       const uint32_t dlo = cut ? ct.hi + 1u : k_lo;
-      if (!find_by_mass<DT>(s, dlo, t, dv, m, h)) return false;
-      dt = tie_group<DT>(s, h, dlo, dv, m);
+      if (find_by_mass<DT>(s, dlo, t, dv, m, h))
+        dt = tie_group<DT>(s, h, dlo, dv, m);
+      else
+        ok = false;
     }
     n_avail = (int)dt.n;
   }
@@ -1444,14 +1487,19 @@ __device__ __forceinline__ bool resolve16(Smem& s, int V, const Divider& dv, int
   st.sel_hi = dt.hi;
   st.sel_n = n_avail;
   st.sel_rank = (int)fmax(0.0, fmin((dt.w > 0.0) ? floor((t - dt.above) / dt.w) : 0.0, (double)(n_avail - 1)));
-  return true;
+  if (lane_id() == 0) {
+    s.res_lo = st.sel_lo;
+    s.res_hi = st.sel_hi;
+    s.res_rank = st.sel_rank;
+    s.res_ok = ok ? 1 : 0;
+  }
 }
 
 // Index of the rank-th lowest-index element whose ord lies in [lo, hi].
 template <int DT, class Src>
 __device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank) {
-  // the searches before this read the histogram wave by wave; the selection reuses it
-  __syncthreads();
+  // the caller's barrier after the searches (which read the histogram) comes first: the
+  // selection reuses it
   if constexpr (Src::kStore) {
     // values of one sign: a contiguous range of raws (non-negative ords lo.. map to raws
     // lo - 0x8000.., negative ones to raws 0xffff - hi ..)
@@ -1610,9 +1658,19 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
       // per-ord masses in fp32 (a u16 count times a weight <= 1), the lane's four summed
       // in fp32, everything above that in fp64
       float pf = 0.0f;
+      if (group_fma16<DT>(g, dv)) {
+        // the common case: one branch for the group, four independent quotients per lane
+        // (an empty ord adds 0 * w = +0, which leaves the sum as it is)
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (n4[k]) pf += (float)n4[k] * weight16f<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
+        for (int k = 0; k < 4; ++k) {
+          const float x = dv.fma_seq(raw_to_float<DT>(raw_of_ord16(g * 256u + 4u * (uint32_t)l + (uint32_t)k)));
+          pf += (float)n4[k] * __builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (n4[k]) pf += (float)n4[k] * weight16f<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
+      }
       double part = (double)pf;
       // subgroups of 32 ords are 8-lane segments: quad sums, then row_shr 4 leaves each
       // segment's sum in its last lane; summed top-down in order, they give the subgroup
@@ -1657,10 +1715,12 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   }
   __syncthreads();
   RowState st;
-  if (!resolve16<DT>(s, V, dv, kk, kc, p, u, m, a.out_info != nullptr, st)) return false;  // a counter wrapped
+  resolve16<DT>(s, V, dv, kk, kc, p, u, m, a.out_info != nullptr, st);
+  __syncthreads();
+  if (!s.res_ok) return false;  // a counter wrapped
 
   // which of the tied tokens: the sel_rank-th lowest index with ord in [sel_lo, sel_hi]
-  const int tok = select_tied16<DT>(src, s, st.sel_lo, st.sel_hi, st.sel_rank);
+  const int tok = select_tied16<DT>(src, s, s.res_lo, s.res_hi, s.res_rank);
   if (threadIdx.x == 0) write_info(a, b, tok < 0 ? 0 : tok, PBS_ROW_OK, st);
   return true;
 }

@@ -172,6 +172,27 @@ def test_counter_wrap_takes_general_path(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_zero_ties_in_a_partial_chunk(dev, dtype):
+    """Register rows whose length leaves the last chunk partly past the row end (those
+    vectors load as zeros) while the draw lands in a tie group of +0: the selection must
+    count only the real zeros. Also a +0 / -0 tie and a row whose tie group excludes 0."""
+    g = torch.Generator().manual_seed(25)
+    V = 5000  # 625 16-byte vectors: the second chunk of 512 lanes is 113 lanes full
+    x = torch.zeros(6, V)
+    x[:, ::50] = -torch.rand(6, 100, generator=g) - 0.5  # a few negatives; the maximum is 0
+    x[2, 1::3] = -0.0                                     # -0 ties with +0
+    x[3] = torch.randn(V, generator=g)                    # no zero ties at the draw
+    x[4, V - 7:] = 0.25                                   # ties at the top in the last vector
+    x[5, :] = 0.0                                         # one tie group of V
+    logits = x.to(dtype)
+    T = [1.0, 0.7, 1.0, 1.1, 1.0, 1.0]
+    K = [0, 0, 0, 0, 3, 0]
+    P = [1.0, 0.9, 1.0, 0.95, 1.0, 1.0]
+    U = [0.7, 0.999, 0.5, 0.3, 0.9, 0.9999]
+    run_case(dev, f"zero_ties_partial_{DT_NAME[dtype]}", logits, T, K, P, U)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_values_colliding_after_division(dev, dtype):
     """A huge temperature sends many distinct 16-bit values to the same (subnormal or zero)
     fp32 quotient: ties that span several histogram bins, including -0 and +0."""
