@@ -1090,11 +1090,10 @@ __device__ __forceinline__ void tie_range16(uint32_t o, const Divider& dv, uint3
 }
 
 // ---------------------------------------------------------------------------------------
-// searches. Wave-local: every wave runs them on the same LDS state and gets the same
-// answer, so they need no barrier. Three levels, in descending ord order: groups of 256
-// ords (count and mass prefix tables), subgroups of 32 ords (masses written by the mass
-// pass; their prefixes are summed here, sequentially, in the same order the group mass
-// was) and single ords (weights computed on the spot).
+// searches. Wave-local: a wave runs them on LDS state no one writes meanwhile, so they
+// need no barrier. Three levels, in descending ord order: groups of 256 ords (count and
+// mass prefix tables), subgroups of 32 ords (the mass above each, from the mass pass) and
+// single ords (weights computed on the spot, one per lane, an fp32 scan).
 // ---------------------------------------------------------------------------------------
 struct BinHit {
   uint32_t o;          // the ord found
@@ -1172,6 +1171,35 @@ __device__ __forceinline__ void bins_count(const Smem& s, uint32_t g, uint32_t n
   o = g * 256u + 252u - 4u * (uint32_t)L + bcast_u32((uint32_t)fi, L);
   cnt = bcast_u32(fc, L);
   above = bcast_u32(fa, L);
+}
+
+// Ords 4l .. 4l+3 of group g for lane l (lanes ascending; from lane 63 down they run
+// from the top): their counts (ords below lo count 0), fp32 weights exp(x - m) and the
+// lane's mass, sum of count * weight with explicit FMAs in ascending ord order, so that
+// every caller gets the same bits. One branch per group takes the FMA division for all
+// four ords when the group's exponents allow it (an empty ord then adds 0 * w = +0).
+template <int DT>
+__device__ __forceinline__ float lane_ords16(const Smem& s, uint32_t g, uint32_t lo, const Divider& dv, float m,
+                                             uint32_t (&n4)[4], float (&w4)[4]) {
+  const uint32_t ob = g * 256u + 4u * (uint32_t)lane_id();
+  counts4(s, ob, n4);
+  if (group_fma16<DT>(g, dv)) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float x = dv.fma_seq(raw_to_float<DT>(raw_of_ord16(ob + (uint32_t)k)));
+      w4[k] = __builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w4[k] = n4[k] ? weight16f<DT>(ob + (uint32_t)k, dv, m) : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (ob + (uint32_t)k < lo) n4[k] = 0u;
+  float lsum = (float)n4[0] * w4[0];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) lsum = __builtin_fmaf((float)n4[k], w4[k], lsum);
+  return lsum;
 }
 
 // mass of the elements of subgroup k of g with ord > o, and the weight of ord o
@@ -1631,7 +1659,7 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   }
 
   // group masses: the non-empty groups from glo up, ranked and dealt round-robin to the
-  // waves; lane l weighs ords 4l .. 4l+3 of the group (the others get mass 0)
+  // waves; lane l weighs ords 4l .. 4l+3 of the group (the other groups get mass 0)
   {
     uint32_t ne = 0u;
 #pragma unroll
@@ -1649,43 +1677,20 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
     for (uint32_t r = (uint32_t)wv; r < total; r += NWAVE) {
       const bool mine = r >= excl && r < incl;
       const int L = first_lane(ballot(mine));
-      // only the owning lane's rank is meaningful (and bounded by its popcount, <= 4)
-      uint32_t bits = ne;
-      for (uint32_t k = mine ? r - excl : 0u; k > 0u; --k) bits &= bits - 1u;
+      // the owning lane's (r - excl)-th set bit of ne (rank <= 3, no loop)
+      const uint32_t k = mine ? r - excl : 0u;
+      const uint32_t b1 = ne & (ne - 1u), b2 = b1 & (b1 - 1u), b3 = b2 & (b2 - 1u);
+      const uint32_t bits = k == 0u ? ne : k == 1u ? b1 : k == 2u ? b2 : b3;
       const uint32_t g = bcast_u32(4u * (uint32_t)l + (uint32_t)(__ffs(bits) - 1), L);
+      // the lanes' masses (fp32) summed by an fp64 wave scan: the group mass is the total
+      // and the mass above subgroup k (ords 32k .. 32k+31, lanes 8k .. 8k+7) is the total
+      // less the scan at lane 8k+7
       uint32_t n4[4];
-      counts4(s, g * 256u + 4u * (uint32_t)l, n4);
-      // per-ord masses in fp32 (a u16 count times a weight <= 1), the lane's four summed
-      // in fp32, everything above that in fp64
-      float pf = 0.0f;
-      if (group_fma16<DT>(g, dv)) {
-        // the common case: one branch for the group, four independent quotients per lane
-        // (an empty ord adds 0 * w = +0, which leaves the sum as it is)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float x = dv.fma_seq(raw_to_float<DT>(raw_of_ord16(g * 256u + 4u * (uint32_t)l + (uint32_t)k)));
-          pf += (float)n4[k] * __builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (n4[k]) pf += (float)n4[k] * weight16f<DT>(g * 256u + 4u * (uint32_t)l + (uint32_t)k, dv, m);
-      }
-      double part = (double)pf;
-      // subgroups of 32 ords are 8-lane segments: quad sums, then row_shr 4 leaves each
-      // segment's sum in its last lane; summed top-down in order, they give the subgroup
-      // prefixes the searches use and the group mass
-      part += dpp_f64<0xb1>(part);  // quad_perm [1,0,3,2]
-      part += dpp_f64<0x4e>(part);  // quad_perm [2,3,0,1]
-      part += dpp_f64<ROW_SHR4>(part);
-      // top-down prefixes of the subgroup masses (lane k writes subgroup k's), then the total
-      double gm = 0.0, my_above = 0.0;
-#pragma unroll
-      for (int k = 7; k >= 0; --k) {
-        my_above = (l == k) ? gm : my_above;
-        gm += bcast_f64(part, 8 * k + 7);
-      }
-      if (l < 8) s.subabove[g * 8u + (uint32_t)l] = my_above;
+      float w4[4];
+      const float pf = lane_ords16<DT>(s, g, 0u, dv, m, n4, w4);
+      const double incl = wscan_f64((double)pf);
+      const double gm = bcast_f64(incl, 63);
+      if ((l & 7) == 7) s.subabove[g * 8u + (uint32_t)(l >> 3)] = gm - incl;
       if (l == 0) s.gmass[g] = gm;
     }
   }
