@@ -300,6 +300,7 @@ __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
 struct Divider {
   float T, r;
   int elo, ehi;  // biased exponents of a for which the FMA sequence is safe
+  int qlo, qhi;  // biased exponents of a whose quotient is certainly normal and finite
   __device__ __forceinline__ void init(float T_) {
     T = T_;
     r = 1.0f / T_;
@@ -311,9 +312,13 @@ struct Divider {
     if (et >= 1 && et <= 250) {
       elo = max(26, et - 100);
       ehi = min(254, et + 125);
+      qlo = max(1, et - 124);
+      qhi = min(254, et + 124);
     } else {
       elo = 1;
       ehi = 0;
+      qlo = 1;
+      qhi = 0;
     }
   }
   // the FMA sequence alone: exact for a with biased exponent in [elo, ehi]
@@ -325,6 +330,9 @@ struct Divider {
     return fmaf(res, r, q);
   }
   __device__ __forceinline__ bool safe_exp(int e) const { return e >= elo && e <= ehi; }
+  // a with biased exponent e in [qlo, qhi] has a normal, finite quotient a / T (its
+  // exponent lies in [e - et + 126, e - et + 128], one step inside the limits)
+  __device__ __forceinline__ bool quotient_normal(int e) const { return e >= qlo && e <= qhi; }
   // operator() behind one wave-uniform branch: the FMA sequence when every active lane
   // may take it (latency-bound code, where per-lane branches cost more than the division)
   __device__ __forceinline__ float uniform(float a) const {
@@ -905,7 +913,10 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
   {
     uint32_t c[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = (4 * l + i < NCH * NWAVE) ? s.hist[4 * l + i] : 0u;
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t hv = s.hist[4 * l + i];  // in range for every lane; masked after the load
+      c[i] = (4 * l + i < NCH * NWAVE) ? hv : 0u;
+    }
     const uint32_t tot = c[0] + c[1] + c[2] + c[3];
     const uint32_t incl = wscan_u32(tot);
     const uint64_t hit = ballot(incl > (uint32_t)rank);
@@ -1060,6 +1071,11 @@ __device__ __forceinline__ float weight16f(uint32_t o, const Divider& dv, float 
 // is monotone, so binary search.
 template <int DT>
 __device__ __forceinline__ void tie_range16(uint32_t o, const Divider& dv, uint32_t& lo, uint32_t& hi) {
+  // most values: a normal quotient, known from the exponents alone (no division)
+  if (dv.quotient_normal((int)((__float_as_uint(raw_to_float<DT>(raw_of_ord16(o))) >> 23) & 0xff))) {
+    lo = hi = o;
+    return;
+  }
   const float x = scaled16<DT>(o, dv);
   const float ax = fabsf(x);
   if (ax >= 1.17549435e-38f && ax <= 3.40282347e38f) {
@@ -1111,7 +1127,10 @@ __device__ __forceinline__ int find_group_count(const Smem& s, uint32_t need) {
 #pragma unroll
   for (int i = 3; i >= 0; --i) {
     const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
-    if (s.gcount[g] && s.gabove_cnt[g] < need) found = (int)g;
+    // both loads unconditional (bitwise and): a short-circuit test would wait for each
+    // load in turn
+    const uint32_t gc = s.gcount[g], ga = s.gabove_cnt[g];
+    if ((gc != 0u) & (ga < need)) found = (int)g;
   }
   // lanes hold ascending groups: the first lane with a hit has the lowest
   const uint64_t hit = ballot(found >= 0);
@@ -1127,7 +1146,8 @@ __device__ __forceinline__ int find_group_mass(const Smem& s, uint32_t lo, doubl
 #pragma unroll
   for (int i = 3; i >= 0; --i) {
     const uint32_t g = 4u * (uint32_t)l + (uint32_t)i;
-    if (g >= glo && s.gmass[g] > 0.0 && s.gabove_mass[g] <= target) found = (int)g;
+    const double gm = s.gmass[g], ga = s.gabove_mass[g];  // unconditional, as above
+    if ((g >= glo) & (gm > 0.0) & (ga <= target)) found = (int)g;
   }
   const uint64_t hit = ballot(found >= 0);
   return hit ? (int)bcast_u32((uint32_t)found, first_lane(hit)) : -1;
@@ -1209,7 +1229,8 @@ __device__ __forceinline__ void mass_above_in_sub(const Smem& s, uint32_t g, uin
                                                   const Divider& dv, float m, double& mass, double& w) {
   const int l = lane_id();
   const uint32_t ol = g * 256u + 32u * k + 31u - (uint32_t)(l & 31);
-  const uint32_t c = (l < 32 && ol > o) ? hist_count(s, ol) : 0u;
+  const uint32_t hc = hist_count(s, ol);  // every lane's ol is in range: load first, then mask
+  const uint32_t c = (l < 32 && ol > o) ? hc : 0u;
   const float part = c ? (float)c * weight16f<DT>(ol, dv, m) : 0.0f;
   mass = (double)bcast_f32(wscan_f32(part), 63);
   w = (double)weight16f<DT>(o, dv, m);
@@ -1256,7 +1277,8 @@ __device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double 
   const uint32_t klo = (g == (lo >> 8)) ? (lo & 255u) >> 5 : 0u;
   const uint32_t kl = (uint32_t)(l & 7);
   const double st_k = s.subabove[g * 8u + kl];
-  const double en_k = kl ? s.subabove[g * 8u + kl - 1u] : s.gmass[g];
+  const double sa_prev = s.subabove[g * 8u + (kl ? kl - 1u : 0u)], gm_g = s.gmass[g];
+  const double en_k = kl ? sa_prev : gm_g;
   const uint64_t ks = ballot(l < 8 && kl >= klo && en_k > st_k && st_k <= r);
   if (!ks) return false;
   const int k = first_lane(ks);
@@ -1270,7 +1292,8 @@ __device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double 
   // ords: lanes 0..31, descending; fp32 masses and scan inside one subgroup (its share of
   // the total is summed in fp64 above)
   const uint32_t ol = g * 256u + 32u * (uint32_t)k + 31u - (uint32_t)(l & 31);
-  const uint32_t c = (l < 32 && ol >= lo) ? hist_count(s, ol) : 0u;
+  const uint32_t hc = hist_count(s, ol);  // every lane's ol is in range: load first, then mask
+  const uint32_t c = (l < 32 && ol >= lo) ? hc : 0u;
   const float wt = c ? weight16f<DT>(ol, dv, m) : 0.0f;
   const float ms = (float)c * wt;
   const float mi = wscan_f32(ms);
@@ -1354,7 +1377,10 @@ __device__ __forceinline__ uint32_t count_ge_local(const Smem& s, uint32_t t) {
   const int l = lane_id();
   uint32_t c = 0u;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c += (4u * (uint32_t)l + (uint32_t)i > g) ? s.gcount[4 * l + i] : 0u;
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t gc = s.gcount[4 * l + i];
+    c += (4u * (uint32_t)l + (uint32_t)i > g) ? gc : 0u;
+  }
   return wsum_u32(c) + count_above_in_group(s, g, t - 1u);
 }
 
@@ -1397,11 +1423,10 @@ __device__ __forceinline__ KthCount kth_by_count(const Smem& s, uint32_t need, c
   return r;
 }
 
-// Top-k threshold, top-p cutoff and draw position from the histogram summaries. Every
-// wave runs it and ends with the same RowState. The searches are wave-local, except that
-// with top-p the cutoff and a guessed draw run side by side on the two halves of the
-// waves (one barrier). Returns false if a u16 counter wrapped (one value more than 65535
-// times): the caller then takes the general path.
+// Top-k threshold, top-p cutoff and draw position from the histogram summaries. With
+// top-p the cutoff and a guessed draw run side by side in waves 0 and 1 (one barrier).
+// s.res_ok = 0 if a u16 counter wrapped (one value more than 65535 times) or a search
+// found nothing: the caller then takes the general path.
 template <int DT>
 __device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int kk, const KthCount& kc, float p,
                                           float u, float m, bool want_info, RowState& st) {
@@ -1606,42 +1631,42 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   __syncthreads();
 
   // Every wave checks the total (a u16 counter wraps only if one value occurs more than
-  // 65535 times: the general path takes such rows), then NaN (multinomial raises on it,
-  // sampling.py:27), then finds the row maximum from the highest non-empty ord.
+  // 65535 times: the general path takes such rows) and NaN (multinomial raises on it,
+  // sampling.py:27), and finds the row maximum from the highest non-empty ord. The three
+  // are independent: all loads first, the tests after the maximum.
+  uint32_t omax;
+  uint32_t total, nan;
   {
-    uint32_t c = 0u;
+    uint32_t gc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c += s.gcount[4 * l + i];
-    if (wsum_u32(c) != (uint32_t)V) return false;
-  }
-  {
+    for (int i = 0; i < 4; ++i) gc[i] = s.gcount[4 * l + i];
     const uint32_t inf_raw = DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
-    const uint32_t nan = s.nan_cnt - hist_count_raw(s, inf_raw) - hist_count_raw(s, inf_raw | 0x8000u);
-    if (nan) {
-      if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NAN, NAN);
-      return true;
-    }
-  }
-  Divider dv;
-  dv.init(T);
-  float m;
-  {
+    nan = s.nan_cnt - hist_count_raw(s, inf_raw) - hist_count_raw(s, inf_raw | 0x8000u);
+    total = wsum_u32((gc[0] + gc[1]) + (gc[2] + gc[3]));
     uint32_t nz = 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) nz |= (s.gcount[4 * l + i] ? 1u : 0u) << i;
+    for (int i = 0; i < 4; ++i) nz |= (gc[i] ? 1u : 0u) << i;
     const uint64_t any = ballot(nz != 0u);
-    const int L = 63 - __clzll((unsigned long long)any);  // the row is not empty
-    const uint32_t g = 4u * (uint32_t)L + (31u - __clz(bcast_u32(nz, L)));
+    // (empty only if counters wrapped, which the total test below catches)
+    const int L = any ? 63 - __clzll((unsigned long long)any) : 0;
+    const uint32_t g = 4u * (uint32_t)L + (31u - __clz(bcast_u32(nz, L) | 1u));
     uint32_t n4[4];
     counts4(s, g * 256u + 4u * (uint32_t)l, n4);
     uint32_t top = 0u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) top = n4[i] ? (uint32_t)i + 1u : top;
     const uint64_t any2 = ballot(top != 0u);
-    const int L2 = 63 - __clzll((unsigned long long)any2);
-    const uint32_t omax = g * 256u + 4u * (uint32_t)L2 + bcast_u32(top, L2) - 1u;
-    m = scaled16<DT>(omax, dv);
+    const int L2 = any2 ? 63 - __clzll((unsigned long long)any2) : 0;
+    omax = g * 256u + 4u * (uint32_t)L2 + max(bcast_u32(top, L2), 1u) - 1u;
   }
+  if (total != (uint32_t)V) return false;
+  if (nan) {
+    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NAN, NAN);
+    return true;
+  }
+  Divider dv;
+  dv.init(T);
+  const float m = scaled16<DT>(omax, dv);
   if (!(m > -INFINITY && m < INFINITY)) {
     if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NONFINITE, m);
     return true;
