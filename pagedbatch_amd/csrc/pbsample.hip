@@ -88,10 +88,22 @@ __device__ __forceinline__ uint32_t wscan_u32(uint32_t v) {
   v += dpp<ROW_BCAST31, 0xc>(v, 0u);
   return v;
 }
+// all rows written, lanes without a source lane read 0 (bound_ctrl): no zeroed old value
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_z(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
+}
 template <int CTRL, int RM = 0xf>
 __device__ __forceinline__ double dpp_f64(double v) {
   const uint64_t b = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = dpp<CTRL, RM>((uint32_t)b, 0u), hi = dpp<CTRL, RM>((uint32_t)(b >> 32), 0u);
+  uint32_t lo, hi;
+  if constexpr (RM == 0xf) {
+    lo = dpp_z<CTRL>((uint32_t)b);
+    hi = dpp_z<CTRL>((uint32_t)(b >> 32));
+  } else {
+    lo = dpp<CTRL, RM>((uint32_t)b, 0u);
+    hi = dpp<CTRL, RM>((uint32_t)(b >> 32), 0u);
+  }
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 __device__ __forceinline__ double wscan_f64(double v) {
@@ -864,9 +876,12 @@ __device__ __forceinline__ u4 pick_chunk(const u4 (&r)[N], int j) {
   return q;
 }
 
+// With `out` (token and status arrays, row b) the lane that finds the element writes the
+// row's result itself and SEL_WRITTEN is returned: no barrier hands the index to wave 0.
+constexpr int SEL_WRITTEN = -2;
 template <bool ORD, int DT, int NCH>
 __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Smem& s, uint32_t lo, uint32_t span,
-                                                  int rank) {
+                                                  int rank, const KArgs* out = nullptr, int b = 0) {
   static_assert(NCH * NWAVE <= 256 && NCH <= 32, "chunk table must fit 4 entries per lane");
   const int l = lane_id(), w = wave_id();
   const uint32_t lo2 = lo | (lo << 16);
@@ -939,7 +954,14 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
     }
   }
   if (pos < 0) {
-    if (threadIdx.x == 0) s.sel_index = -1;
+    if (threadIdx.x == 0) {
+      if (out) {
+        out->out_token[b] = 0;
+        out->out_status[b] = PBS_ROW_OK;
+      } else {
+        s.sel_index = -1;
+      }
+    }
   } else {
     const int jstar = pos / NWAVE, wstar = pos % NWAVE;
     if (w == wstar) {
@@ -949,12 +971,19 @@ __device__ __forceinline__ int select_index_reg16(const RegRow<DT, NCH>& src, Sm
       const uint32_t incl = wscan_u32(cnt);
       const uint32_t excl = incl - cnt;
       if ((uint32_t)rr >= excl && (uint32_t)rr < incl) {
-        uint32_t b = bits;
-        for (uint32_t k = (uint32_t)rr - excl; k > 0; --k) b &= b - 1u;
-        s.sel_index = (jstar * NT + (int)threadIdx.x) * 8 + (__ffs(b) - 1);
+        uint32_t mb = bits;
+        for (uint32_t k = (uint32_t)rr - excl; k > 0; --k) mb &= mb - 1u;
+        const int idx = (jstar * NT + (int)threadIdx.x) * 8 + (__ffs(mb) - 1);
+        if (out) {
+          out->out_token[b] = idx;
+          out->out_status[b] = PBS_ROW_OK;
+        } else {
+          s.sel_index = idx;
+        }
       }
     }
   }
+  if (out) return SEL_WRITTEN;
   __syncthreads();
   const int r = s.sel_index;
   __syncthreads();
@@ -1550,14 +1579,15 @@ __device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int
 
 // Index of the rank-th lowest-index element whose ord lies in [lo, hi].
 template <int DT, class Src>
-__device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank) {
+__device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t lo, uint32_t hi, int rank,
+                                             const KArgs* out = nullptr, int b = 0) {
   // the caller's barrier after the searches (which read the histogram) comes first: the
   // selection reuses it
   if constexpr (Src::kStore) {
     // values of one sign: a contiguous range of raws (non-negative ords lo.. map to raws
     // lo - 0x8000.., negative ones to raws 0xffff - hi ..)
     if (lo >= 0x8000u || hi < 0x8000u)
-      return select_index_reg16<false>(src, s, lo >= 0x8000u ? lo - 0x8000u : 0xffffu - hi, hi - lo, rank);
+      return select_index_reg16<false>(src, s, lo >= 0x8000u ? lo - 0x8000u : 0xffffu - hi, hi - lo, rank, out, b);
     // a range taking in both -0 and +0 (rare): the general selection on ords
     return select_index<DT>(src, s, [=](uint32_t raw) { return ord16u(raw) - lo <= hi - lo; }, rank);
   } else {
@@ -1750,8 +1780,9 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   if (!s.res_ok) return false;  // a counter wrapped
 
   // which of the tied tokens: the sel_rank-th lowest index with ord in [sel_lo, sel_hi]
-  const int tok = select_tied16<DT>(src, s, s.res_lo, s.res_hi, s.res_rank);
-  if (threadIdx.x == 0) write_info(a, b, tok < 0 ? 0 : tok, PBS_ROW_OK, st);
+  // without diagnostics the selecting lane writes the token itself
+  const int tok = select_tied16<DT>(src, s, s.res_lo, s.res_hi, s.res_rank, a.out_info ? nullptr : &a, b);
+  if (tok != SEL_WRITTEN && threadIdx.x == 0) write_info(a, b, tok < 0 ? 0 : tok, PBS_ROW_OK, st);
   return true;
 }
 
