@@ -40,6 +40,11 @@ def run_case(dev, name, logits_cpu, T, K, P, U, row_map=None, want_probs=True, i
     rep = compare_rows(out.tokens, out.status, refs, greedy, probs=probs, kept=kept, info=out.info)
     print(f"[case] {name}: {rep.summary()}", flush=True)
     assert rep.ok(), rep.summary()
+    # the plain call (no diagnostics: the selecting lane writes the token itself) must give
+    # the same tokens and statuses as the diagnostic call checked above
+    tok, st = sample_arrays(x, T, K, P, U, row_map=row_map)
+    np.testing.assert_array_equal(np.asarray(tok), np.asarray(out.tokens))
+    np.testing.assert_array_equal(np.asarray(st), np.asarray(out.status))
     return out, refs, rep
 
 
