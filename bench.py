@@ -145,6 +145,24 @@ def engine_step(args):
 
     b, r = split(tb), split(tr)
     step_ms = b["forward_ms"] + b["sample_ms"]
+
+    # the step's stop check (engine.py:173-182) for its 64 rows on the device: one kernel
+    # from device tokens and one copy back, timed from launch to the reasons on the host
+    import time
+
+    from pagedbatch_amd.finish import FinishRule, finish_codes
+
+    dev = torch.device("cuda", 0)
+    toks = torch.tensor([o[-1] for o in out_b], dtype=torch.int32, device=dev)
+    rules = [FinishRule(ignore_eos=False, stop_token_ids=(), num_output=128, max_tokens=128, num_tokens=256)
+             for _ in out_b]
+    fin = []
+    for i in range(25):
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        codes = finish_codes(toks, rules, None, 2048).cpu()
+        fin.append(time.perf_counter() - t0)
+    assert (codes == 2).all()  # every request has its 128 outputs: "length"
     line = {
         "metric": "engine decode tokens/s (smollm2-135m-random bf16, 64 requests, 128 prompt + 128 output tokens)",
         "value": round(64 / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": b["decode_steps"],
@@ -153,6 +171,7 @@ def engine_step(args):
         "config": {"workload": "engine_step_smollm2", "requests": 64, "prompt_len": 128, "output_len": 128,
                    "block_size": 16, "mix": "half greedy, half top_k=50 top_p=0.9 T=1.0"},
         "batched_sampling": b, "per_row_sampling": r, "same_tokens_batched_vs_per_row": same,
+        "finish_check_us": round(1e6 * sorted(fin[5:])[len(fin[5:]) // 2], 1),
         "torch": torch.__version__,
     }
     print(json.dumps(line), flush=True)

@@ -135,6 +135,40 @@ int pbs_sample_debug(const void* logits, int dtype, int64_t n_logit_rows, int64_
                      int32_t* out_token, int32_t* out_status, float* out_probs, uint8_t* out_kept,
                      pbs_row_info* out_info, void* workspace, size_t workspace_bytes, void* stream);
 
+/* finish reasons written by pbs_finish_reasons */
+enum {
+  PBS_FINISH_NONE = 0,
+  PBS_FINISH_STOP = 1,       /* "stop" */
+  PBS_FINISH_LENGTH = 2      /* "length" */
+};
+
+/*
+ * The finish reason of each sampled sequence after its new token, computed on the device
+ * so that the engine reads tokens and reasons back in one copy instead of inspecting
+ * each token on the host. Replaces pagedbatch/engine.py:173-182 (Engine._finish_reason),
+ * called per sampled row at engine.py:149 after the token is appended:
+ *   STOP    if !ignore_eos[b] and (tokens[b] == eos_token_id or tokens[b] is one of row
+ *           b's stop ids)
+ *   LENGTH  otherwise, if num_output[b] >= max_tokens[b] or num_tokens[b] >= max_model_len
+ *   NONE    otherwise
+ *   tokens        device int32[rows] (pbs_sample's out_token)
+ *   eos_token_id  the model's EOS id (ModelConfig.eos_token_id), -1 for none
+ *   ignore_eos    device uint8[rows]   (SamplingParams.ignore_eos)
+ *   stop_offsets  device int32[rows + 1]: row b's stop ids are
+ *                 stop_ids[stop_offsets[b] .. stop_offsets[b + 1])
+ *   stop_ids      device int32[stop_offsets[rows]] (SamplingParams.stop_token_ids); may
+ *                 be NULL when no row has any
+ *   num_output    device int32[rows]   output tokens of the sequence, this one included
+ *   max_tokens    device int32[rows]   (SamplingParams.max_tokens)
+ *   num_tokens    device int32[rows]   prompt + output tokens, this one included
+ *   max_model_len EngineConfig.max_model_len
+ *   out_reason    device int32[rows]   PBS_FINISH_* codes
+ */
+int pbs_finish_reasons(const int32_t* tokens, int64_t rows, int32_t eos_token_id, const uint8_t* ignore_eos,
+                       const int32_t* stop_offsets, const int32_t* stop_ids, const int32_t* num_output,
+                       const int32_t* max_tokens, const int32_t* num_tokens, int32_t max_model_len,
+                       int32_t* out_reason, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

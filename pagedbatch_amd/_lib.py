@@ -32,8 +32,12 @@ ERR_WORKSPACE = -4
 # per-row status (PBS_ROW_*)
 ROW_OK, ROW_NAN, ROW_NONFINITE, ROW_BAD_PARAM = 0, 1, 2, 3
 
+# finish reasons (PBS_FINISH_*)
+FINISH_NONE, FINISH_STOP, FINISH_LENGTH = 0, 1, 2
+
 # the C symbols include/pbsample.h declares, in declaration order
-SYMBOLS = ("pbs_abi_version", "pbs_last_error", "pbs_workspace_bytes", "pbs_sample", "pbs_sample_debug")
+SYMBOLS = ("pbs_abi_version", "pbs_last_error", "pbs_workspace_bytes", "pbs_sample", "pbs_sample_debug",
+           "pbs_finish_reasons")
 
 # layout of pbs_row_info
 ROW_INFO_DTYPE = np.dtype(
@@ -110,6 +114,21 @@ def load(path: str | None = None):
             _c.c_void_p,  # out_info
             _c.c_void_p,  # workspace
             _c.c_size_t,  # workspace_bytes
+            _c.c_void_p,  # stream
+        ]
+        lib.pbs_finish_reasons.restype = _c.c_int
+        lib.pbs_finish_reasons.argtypes = [
+            _c.c_void_p,  # tokens
+            _c.c_int64,  # rows
+            _c.c_int32,  # eos_token_id
+            _c.c_void_p,  # ignore_eos
+            _c.c_void_p,  # stop_offsets
+            _c.c_void_p,  # stop_ids
+            _c.c_void_p,  # num_output
+            _c.c_void_p,  # max_tokens
+            _c.c_void_p,  # num_tokens
+            _c.c_int32,  # max_model_len
+            _c.c_void_p,  # out_reason
             _c.c_void_p,  # stream
         ]
         v = lib.pbs_abi_version()

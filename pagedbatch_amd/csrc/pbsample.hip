@@ -2820,6 +2820,39 @@ __global__ __launch_bounds__(NT) void k_sample(KArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Finish reasons after a step's tokens (pagedbatch/engine.py:173-182): one thread per
+// sequence, reading the token the sampler wrote and the sequence's stop rule.
+// ---------------------------------------------------------------------------------------
+struct FinishArgs {
+  const int32_t* tokens;
+  int64_t rows;
+  int32_t eos;  // -1: the model has none
+  const uint8_t* ignore_eos;
+  const int32_t* stop_offsets;
+  const int32_t* stop_ids;
+  const int32_t* num_output;
+  const int32_t* max_tokens;
+  const int32_t* num_tokens;
+  int32_t max_model_len;
+  int32_t* out_reason;
+};
+
+__global__ __launch_bounds__(256) void k_finish(FinishArgs f) {
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (b >= f.rows) return;
+  const int32_t tok = f.tokens[b];
+  int32_t reason = PBS_FINISH_NONE;
+  if (!f.ignore_eos[b]) {
+    bool stop = f.eos >= 0 && tok == f.eos;
+    for (int32_t i = f.stop_offsets[b]; i < f.stop_offsets[b + 1] && !stop; ++i) stop = f.stop_ids[i] == tok;
+    if (stop) reason = PBS_FINISH_STOP;
+  }
+  if (reason == PBS_FINISH_NONE && (f.num_output[b] >= f.max_tokens[b] || f.num_tokens[b] >= f.max_model_len))
+    reason = PBS_FINISH_LENGTH;
+  f.out_reason[b] = reason;
+}
+
 }  // namespace pbs
 
 // =========================================================================================
@@ -2946,6 +2979,34 @@ int pbs_sample_debug(const void* logits, int dtype, int64_t n_logit_rows, int64_
   (void)workspace_bytes;
   return sample_impl(logits, dtype, n_logit_rows, rows, vocab, row_stride, row_map, temperature, top_k, top_p,
                      uniform, out_token, out_status, out_probs, out_kept, out_info, stream);
+}
+
+int pbs_finish_reasons(const int32_t* tokens, int64_t rows, int32_t eos_token_id, const uint8_t* ignore_eos,
+                       const int32_t* stop_offsets, const int32_t* stop_ids, const int32_t* num_output,
+                       const int32_t* max_tokens, const int32_t* num_tokens, int32_t max_model_len,
+                       int32_t* out_reason, void* stream) {
+  if (rows < 0) return fail(PBS_ERR_INVALID_ARGUMENT, "rows is negative (%lld)", (long long)rows);
+  if (rows > ((int64_t)1 << 31)) return fail(PBS_ERR_INVALID_ARGUMENT, "rows (%lld) above 2^31", (long long)rows);
+  if (rows == 0) return PBS_OK;
+  if (!tokens || !ignore_eos || !stop_offsets || !num_output || !max_tokens || !num_tokens || !out_reason)
+    return fail(PBS_ERR_INVALID_ARGUMENT, "null device pointer among the required arguments");
+  if (eos_token_id < -1) return fail(PBS_ERR_INVALID_ARGUMENT, "eos_token_id below -1 (%d)", eos_token_id);
+  pbs::FinishArgs f;
+  f.tokens = tokens;
+  f.rows = rows;
+  f.eos = eos_token_id;
+  f.ignore_eos = ignore_eos;
+  f.stop_offsets = stop_offsets;
+  f.stop_ids = stop_ids;
+  f.num_output = num_output;
+  f.max_tokens = max_tokens;
+  f.num_tokens = num_tokens;
+  f.max_model_len = max_model_len;
+  f.out_reason = out_reason;
+  hipLaunchKernelGGL(pbs::k_finish, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, (hipStream_t)stream, f);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return PBS_OK;
 }
 
 }  // extern "C"
