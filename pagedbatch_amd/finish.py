@@ -74,8 +74,8 @@ def finish_codes(tokens: torch.Tensor, rules: Sequence[FinishRule], eos_token_id
         i32 + 4 * (3 * n + 1), int(max_model_len), out.data_ptr(), stream)
     if rc != _lib.OK:
         raise SamplerError(f"pbs_finish_reasons failed ({rc}): {_lib.last_error(lib)}")
-    # keep the staging alive until the kernel has read it
-    out._pbs_staging = (h, d)  # type: ignore[attr-defined]
+    # h and d may go now: torch's host allocator holds pinned blocks until their copies
+    # complete, and its device allocator reuses d only for later work on this stream
     return out
 
 
