@@ -1291,27 +1291,13 @@ __device__ __forceinline__ bool find_by_count(const Smem& s, uint32_t need, cons
   return true;
 }
 
-// the first ord >= lo (descending) whose cumulative mass from the top exceeds target; if
-// rounding keeps the cumulative at or below it, the lowest ord >= lo with mass there
+// The ord level of a search: subgroup k of group g, whose share of the target is
+// r - start (r: the target less the mass above the group, start: the mass above the
+// subgroup in the group).
 template <int DT>
-__device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double target, const Divider& dv, float m,
-                                             BinHit& h) {
-  const int gi = find_group_mass(s, lo, target);
-  if (gi < 0) return false;
-  const uint32_t g = (uint32_t)gi;
-  const double r = target - s.gabove_mass[g];
+__device__ __forceinline__ bool find_in_sub(const Smem& s, uint32_t lo, uint32_t g, int k, double r, double start,
+                                            const Divider& dv, float m, BinHit& h) {
   const int l = lane_id();
-  // subgroup (lanes 0..7, one each): the lowest one in range, with mass, whose interval
-  // [above_k, above_{k-1}) starts at or before r; the intervals tile the group exactly
-  const uint32_t klo = (g == (lo >> 8)) ? (lo & 255u) >> 5 : 0u;
-  const uint32_t kl = (uint32_t)(l & 7);
-  const double st_k = s.subabove[g * 8u + kl];
-  const double sa_prev = s.subabove[g * 8u + (kl ? kl - 1u : 0u)], gm_g = s.gmass[g];
-  const double en_k = kl ? sa_prev : gm_g;
-  const uint64_t ks = ballot(l < 8 && kl >= klo && en_k > st_k && st_k <= r);
-  if (!ks) return false;
-  const int k = first_lane(ks);
-  const double start = bcast_f64(st_k, k);
   // elements above the subgroup in the group (independent of the bin search below)
   uint32_t n4[4];
   counts4(s, g * 256u + 4u * (uint32_t)l, n4);
@@ -1341,6 +1327,44 @@ __device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double 
   h.mass_above = s.gabove_mass[g] + start + (double)bcast_f32(mi - ms, L);
   h.cnt_above = s.gabove_cnt[g] + wsum_u32(ca) + bcast_u32(ci - c, L);
   return true;
+}
+
+// the first ord >= lo (descending) whose cumulative mass from the top exceeds target; if
+// rounding keeps the cumulative at or below it, the lowest ord >= lo with mass there
+template <int DT>
+__device__ __forceinline__ bool find_by_mass(const Smem& s, uint32_t lo, double target, const Divider& dv, float m,
+                                             BinHit& h) {
+  const int gi = find_group_mass(s, lo, target);
+  if (gi < 0) return false;
+  const uint32_t g = (uint32_t)gi;
+  const double r = target - s.gabove_mass[g];
+  const int l = lane_id();
+  // subgroup (lanes 0..7, one each): the lowest one in range, with mass, whose interval
+  // [above_k, above_{k-1}) starts at or before r; the intervals tile the group exactly
+  const uint32_t klo = (g == (lo >> 8)) ? (lo & 255u) >> 5 : 0u;
+  const uint32_t kl = (uint32_t)(l & 7);
+  const double st_k = s.subabove[g * 8u + kl];
+  const double sa_prev = s.subabove[g * 8u + (kl ? kl - 1u : 0u)], gm_g = s.gmass[g];
+  const double en_k = kl ? sa_prev : gm_g;
+  const uint64_t ks = ballot(l < 8 && kl >= klo && en_k > st_k && st_k <= r);
+  if (!ks) return false;
+  const int k = first_lane(ks);
+  const double start = bcast_f64(st_k, k);
+  return find_in_sub<DT>(s, lo, g, k, r, start, dv, m, h);
+}
+
+// The same search when the answer is expected in subgroup k of group g (the tie group
+// after a known one): false, with nothing found, unless the target lies in that
+// subgroup's interval, which is then the one find_by_mass would pick.
+template <int DT>
+__device__ __forceinline__ bool find_by_mass_near(const Smem& s, uint32_t lo, double target, uint32_t g, uint32_t k,
+                                                  const Divider& dv, float m, BinHit& h) {
+  const double r = target - s.gabove_mass[g];
+  const double st = s.subabove[g * 8u + k];
+  const double sa_prev = s.subabove[g * 8u + (k ? k - 1u : 0u)], gm_g = s.gmass[g];
+  const double en = k ? sa_prev : gm_g;
+  if (!(r >= st && r < en)) return false;
+  return find_in_sub<DT>(s, lo, g, (int)k, r, st, dv, m, h);
 }
 
 // count and mass of the elements with ord >= t (whole wave; the rare tie-range path)
@@ -1557,8 +1581,13 @@ __device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int
     if (cut && have_guess && guess.lo > ct.hi && t >= guess.above && t < guess.above + (double)guess.n * guess.w) {
       dt = guess;
     } else {
+      // below the guess (u Z_P past its tie group): first the guess's own subgroup, which
+      // skips the group and subgroup levels when the target lies there
       const uint32_t dlo = cut ? ct.hi + 1u : k_lo;
-      if (find_by_mass<DT>(s, dlo, t, dv, m, h))
+      bool found = cut && have_guess && guess.lo > ct.hi && t >= guess.above &&
+                   find_by_mass_near<DT>(s, dlo, t, guess.lo >> 8, (guess.lo & 255u) >> 5, dv, m, h);
+      if (!found) found = find_by_mass<DT>(s, dlo, t, dv, m, h);
+      if (found)
         dt = tie_group<DT>(s, h, dlo, dv, m);
       else
         ok = false;
