@@ -2688,7 +2688,15 @@ template <int DT, class Src>
 __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, int b) {
   constexpr int EPV = DTraits<DT>::EPV;
   constexpr bool B16 = DTraits<DT>::B16;
-  const int64_t lrow = a.row_map ? (int64_t)a.row_map[b] : (int64_t)b;
+  const size_t elt = B16 ? 2 : 4;
+  // Without a row map the logits row is b (the host checked rows <= n_logit_rows): its
+  // first loads go out before the row's parameters arrive, not after.
+  const bool mapped = a.row_map != nullptr;
+  if (!mapped) {
+    src.init((const uint8_t*)a.logits + (size_t)b * (size_t)a.row_stride * elt, a.nvec, a.vocab);
+    src.load();
+  }
+  const int64_t lrow = mapped ? (int64_t)a.row_map[b] : (int64_t)b;
   const float T = a.temperature[b];
   const int kk = a.top_k[b];
   const float p = a.top_p[b];
@@ -2700,9 +2708,10 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
     if (threadIdx.x == 0) write_error(a, b, PBS_ROW_BAD_PARAM, NAN);
     return;
   }
-  const size_t elt = B16 ? 2 : 4;
-  src.init((const uint8_t*)a.logits + (size_t)lrow * (size_t)a.row_stride * elt, a.nvec, a.vocab);
-  src.load();
+  if (mapped) {
+    src.init((const uint8_t*)a.logits + (size_t)lrow * (size_t)a.row_stride * elt, a.nvec, a.vocab);
+    src.load();
+  }
 
   if (greedy) {
     // torch.argmax (sampling.py:13): first NaN if any, else the first maximum
