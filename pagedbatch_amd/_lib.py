@@ -35,6 +35,9 @@ ROW_OK, ROW_NAN, ROW_NONFINITE, ROW_BAD_PARAM = 0, 1, 2, 3
 # finish reasons (PBS_FINISH_*)
 FINISH_NONE, FINISH_STOP, FINISH_LENGTH = 0, 1, 2
 
+# the C symbols include/pbattn.h declares
+ATTN_SYMBOLS = ("pba_decode_attention",)
+
 # the C symbols include/pbsample.h declares, in declaration order
 SYMBOLS = ("pbs_abi_version", "pbs_last_error", "pbs_workspace_bytes", "pbs_sample", "pbs_sample_debug",
            "pbs_finish_reasons")
@@ -129,6 +132,25 @@ def load(path: str | None = None):
             _c.c_void_p,  # num_tokens
             _c.c_int32,  # max_model_len
             _c.c_void_p,  # out_reason
+            _c.c_void_p,  # stream
+        ]
+        lib.pba_decode_attention.restype = _c.c_int
+        lib.pba_decode_attention.argtypes = [
+            _c.c_void_p,  # q
+            _c.c_void_p,  # k_cache
+            _c.c_void_p,  # v_cache
+            _c.c_int64,  # n_slots
+            _c.c_void_p,  # block_table
+            _c.c_int64,  # max_blocks
+            _c.c_void_p,  # context_lens
+            _c.c_int64,  # rows
+            _c.c_int,  # n_heads
+            _c.c_int,  # n_kv_heads
+            _c.c_int,  # head_dim
+            _c.c_int,  # block_size
+            _c.c_int,  # max_context
+            _c.c_float,  # scale
+            _c.c_void_p,  # out
             _c.c_void_p,  # stream
         ]
         v = lib.pbs_abi_version()

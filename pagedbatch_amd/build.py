@@ -1,6 +1,7 @@
 """Build libpbsample.so in-tree with hipcc for gfx950.
 
-``python -m pagedbatch_amd.build`` compiles ``csrc/pbsample.hip`` into
+``python -m pagedbatch_amd.build`` compiles ``csrc/pbsample.hip`` (the sampler) and
+``csrc/pbattn.hip`` (the paged-attention decode kernel) into
 ``pagedbatch_amd/libpbsample.so`` (the file ``_lib.py`` loads). Packed-FP32 instruction
 selection is disabled (``-packed-fp32-ops``); the kernels are written for wave64 gfx950
 and nothing else.
@@ -16,6 +17,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "pbsample.hip")
+SRCS = [SRC, os.path.join(HERE, "csrc", "pbattn.hip")]
 OUT = os.path.join(HERE, "libpbsample.so")
 ARCH = os.environ.get("PBS_OFFLOAD_ARCH", "gfx950")
 
@@ -38,7 +40,7 @@ def command(out: str = OUT) -> list[str]:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"),
         "-o", out,
-        SRC,
+        *SRCS,
     ]
 
 

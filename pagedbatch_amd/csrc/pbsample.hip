@@ -2985,6 +2985,11 @@ int sample_impl(const void* logits, int dtype, int64_t n_logit_rows, int64_t row
 
 }  // namespace
 
+namespace pbs {
+// error reporting for the library's other translation units (pbs_last_error reads it)
+int report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace pbs
+
 extern "C" {
 
 int pbs_abi_version(void) { return PBS_ABI_VERSION; }

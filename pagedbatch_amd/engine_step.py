@@ -24,6 +24,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from .attention import decode_attention
 from .config import SamplingParams
 from .sampling import sample
 
@@ -97,10 +98,12 @@ class Model:
 
     @torch.no_grad()
     def forward(self, tokens: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor, seq_slots: torch.Tensor,
-                q_len: int, cache: "PagedKV") -> torch.Tensor:
+                q_len: int, cache: "PagedKV", fused_decode: bool = False) -> torch.Tensor:
         """``tokens``/``pos``/``slots``: [B * q_len] (sequence-major); ``seq_slots``: [B, L] the
         cache slots of each sequence's whole context, new tokens last. Returns [B, vocab]
-        logits of each sequence's last token."""
+        logits of each sequence's last token. ``fused_decode`` runs decode steps
+        (``q_len == 1``) through the paged-attention kernel (``attention.decode_attention``)
+        instead of the gather + matmul + softmax below."""
         s = self.shape
         D, Hq, Hkv = s.head_dim, s.num_heads, s.num_kv_heads
         B, L = seq_slots.shape
@@ -119,15 +122,20 @@ class Model:
             q, k = self._rope(q, pos), self._rope(k, pos)
             cache.k[li].index_copy_(0, slots, k.to(cache.k[li].dtype))
             cache.v[li].index_copy_(0, slots, v)
-            # attention in fp32 with contiguous operands: [B, Hkv, rep, q_len, D] x [B, Hkv, D, L]
-            keys = cache.k[li][seq_slots].float().permute(0, 2, 3, 1).contiguous()  # [B, Hkv, D, L]
-            vals = cache.v[li][seq_slots].float().permute(0, 2, 1, 3).contiguous()  # [B, Hkv, L, D]
-            qh = q.view(B, q_len, Hkv, Hq // Hkv, D).permute(0, 2, 3, 1, 4).reshape(B, Hkv, -1, D).contiguous()
-            att = torch.matmul(qh, keys) * scale  # [B, Hkv, rep * q_len, L]
-            if causal is not None:
-                att = att.view(B, Hkv, Hq // Hkv, q_len, L).masked_fill(causal, float("-inf")).view(B, Hkv, -1, L)
-            o = torch.matmul(torch.softmax(att, dim=-1), vals)  # [B, Hkv, rep * q_len, D]
-            o = o.view(B, Hkv, Hq // Hkv, q_len, D).permute(0, 3, 1, 2, 4).reshape(B * q_len, Hq * D)
+            if fused_decode and q_len == 1:
+                o = decode_attention(q.contiguous(), cache.k[li], cache.v[li], cache.block_table_i32,
+                                     torch.full((B,), L, dtype=torch.int32, device=x.device), cache.block_size,
+                                     L, scale).view(B, Hq * D)
+            else:
+                # attention in fp32 with contiguous operands: [B, Hkv, rep, q_len, D] x [B, Hkv, D, L]
+                keys = cache.k[li][seq_slots].float().permute(0, 2, 3, 1).contiguous()  # [B, Hkv, D, L]
+                vals = cache.v[li][seq_slots].float().permute(0, 2, 1, 3).contiguous()  # [B, Hkv, L, D]
+                qh = q.view(B, q_len, Hkv, Hq // Hkv, D).permute(0, 2, 3, 1, 4).reshape(B, Hkv, -1, D).contiguous()
+                att = torch.matmul(qh, keys) * scale  # [B, Hkv, rep * q_len, L]
+                if causal is not None:
+                    att = att.view(B, Hkv, Hq // Hkv, q_len, L).masked_fill(causal, float("-inf")).view(B, Hkv, -1, L)
+                o = torch.matmul(torch.softmax(att, dim=-1), vals)  # [B, Hkv, rep * q_len, D]
+                o = o.view(B, Hkv, Hq // Hkv, q_len, D).permute(0, 3, 1, 2, 4).reshape(B * q_len, Hq * D)
             x = x + o.to(x.dtype) @ p["o"]
             h = self._rms(x, p["ln2"])
             gu = h @ p["gate_up"]
@@ -152,6 +160,7 @@ class PagedKV:
         # so that a sequence's blocks are not contiguous in the pool)
         self.block_table = torch.arange(blocks_per_seq, device=device).view(1, -1) * num_seqs + \
             torch.arange(num_seqs, device=device).view(-1, 1)
+        self.block_table_i32 = self.block_table.to(torch.int32).contiguous()
 
     def slots(self, seq: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """Slots of positions ``pos`` of sequences ``seq`` (broadcast)."""
@@ -174,12 +183,14 @@ class StepTimes:
 
 
 def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len: int = 128, block_size: int = 16,
-        device: str | torch.device = "cuda", seed: int = 0, per_row: bool = False) -> tuple[StepTimes, list[list[int]]]:
+        device: str | torch.device = "cuda", seed: int = 0, per_row: bool = False,
+        fused_decode: bool = False) -> tuple[StepTimes, list[list[int]]]:
     """Prefill every prompt, then decode in lockstep until each request has ``output_len``
     tokens. Half the requests are greedy, half top-k=50 / top-p=0.9 at temperature 1.0; the
     unseeded ones share one engine generator (engine.py:58). ``per_row`` samples with one
     ``sample_token`` call per sequence (the reference loop, unhoisted) instead of one batched
-    ``sample``. Returns the time split and the generated tokens."""
+    ``sample``; ``fused_decode`` runs the decode steps' attention through the paged-attention
+    kernel. Returns the time split and the generated tokens."""
     device = torch.device(device)
     model = Model(shape, device, seed=seed)
     cache = PagedKV(shape, num_seqs, prompt_len + output_len, block_size, device, torch.bfloat16)
@@ -200,7 +211,7 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
         seq_slots = cache.slots(seq.view(-1, 1), ctx)
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
-        logits = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache)
+        logits = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache, fused_decode)
         torch.cuda.synchronize(device)
         t1 = time.perf_counter()
         if per_row:

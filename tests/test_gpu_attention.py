@@ -1,0 +1,93 @@
+"""Paged-attention decode kernel (pagedbatch/model.py:201-224) against the torch fp32
+attention of the engine-step harness on the same cache, and the engine step run both ways."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from pagedbatch_amd import _lib
+
+
+def _torch_decode(q, kc, vc, block_table, lens, block_size, scale):
+    """fp32 reference: gather each sequence's context through its block table, repeat the
+    KV heads (model.py:214-216), softmax(q k^T * scale) v."""
+    B, Hq, D = q.shape
+    Hkv = kc.shape[1]
+    rep = Hq // Hkv
+    out = torch.empty(B, Hq, D, dtype=torch.float32)
+    for b in range(B):
+        L = int(lens[b])
+        t = torch.arange(L)
+        slots = block_table[b, t // block_size].long() * block_size + t % block_size
+        k = kc[slots].float().repeat_interleave(rep, dim=1)  # [L, Hq, D]
+        v = vc[slots].float().repeat_interleave(rep, dim=1)
+        att = torch.einsum("hd,lhd->hl", q[b].float(), k) * scale
+        out[b] = torch.einsum("hl,lhd->hd", torch.softmax(att, dim=-1), v)
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed", [(4, 9, 3, 16, 200, 1), (3, 8, 8, 8, 37, 2), (2, 16, 2, 32, 1500, 3),
+                                                   (5, 4, 1, 16, 1, 4)])
+def test_decode_matches_torch(B, Hq, Hkv, bs, maxL, seed):
+    from pagedbatch_amd.attention import decode_attention
+
+    print(f"[case] decode B={B} Hq={Hq} Hkv={Hkv} bs={bs} maxL={maxL}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    D = 64
+    nblk = (maxL + bs - 1) // bs
+    n_slots = B * nblk * bs + 3 * bs
+    kc = (torch.randn(n_slots, Hkv, D, generator=g) * 0.5).to(torch.bfloat16)
+    vc = torch.randn(n_slots, Hkv, D, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(n_slots // bs, generator=g)[: B * nblk].view(B, nblk).to(torch.int32)
+    lens = torch.randint(1, maxL + 1, (B,), generator=g).to(torch.int32)
+    lens[0] = maxL
+    q = torch.randn(B, Hq, D, generator=g)
+    scale = 1.0 / math.sqrt(D)
+    want = _torch_decode(q, kc, vc, perm, lens, bs, scale)
+    dev = torch.device("cuda", 0)
+    got = decode_attention(q.to(dev), kc.to(dev), vc.to(dev), perm.to(dev), lens.to(dev), bs, maxL, scale).cpu()
+    torch.testing.assert_close(got, want, rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.gpu
+def test_decode_corrupt_block_table_gives_nan_not_a_fault():
+    from pagedbatch_amd.attention import decode_attention
+
+    dev = torch.device("cuda", 0)
+    kc = torch.zeros(64, 1, 64, dtype=torch.bfloat16, device=dev)
+    bt = torch.tensor([[0, 1], [0, 99]], dtype=torch.int32, device=dev)  # block 99 is past the 64 slots
+    lens = torch.tensor([20, 20], dtype=torch.int32, device=dev)
+    out = decode_attention(torch.ones(2, 2, 64, device=dev), kc, kc, bt, lens, 16, 32).cpu()
+    assert torch.isfinite(out[0]).all() and torch.isnan(out[1]).all()
+
+
+@pytest.mark.gpu
+def test_engine_decode_step_fused_matches_unfused():
+    """One decode step of the tiny engine model on the same cache, attention fused or not:
+    the same logits up to the bf16 rounding of the attention output (model.py:224's
+    o_proj input), which is where the two fp32 results can first differ."""
+    from pagedbatch_amd import engine_step as es
+
+    dev = torch.device("cuda", 0)
+    # a small model with the kernel's head_dim of 64
+    shape = es.ModelShape(vocab_size=512, hidden_size=256, intermediate_size=256, num_layers=2, num_heads=4,
+                          num_kv_heads=2)
+    model = es.Model(shape, dev, seed=3)
+    B, P, bs = 5, 21, 8
+    cache = es.PagedKV(shape, B, P + 4, bs, dev, torch.bfloat16)
+    seq = torch.arange(B, device=dev).view(-1, 1)
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, shape.vocab_size, (B, P), generator=g).to(dev)
+    pos = torch.arange(P, device=dev).view(1, -1).expand(B, -1)
+    model.forward(prompt.reshape(-1), pos.reshape(-1), cache.slots(seq, pos).reshape(-1), cache.slots(seq, pos), P, cache)
+    tok = torch.randint(0, shape.vocab_size, (B, 1), generator=g).to(dev)
+    pos1 = torch.full((B, 1), P, device=dev)
+    ctx = torch.arange(P + 1, device=dev).view(1, -1).expand(B, -1)
+    args = (tok.reshape(-1), pos1.reshape(-1), cache.slots(seq, pos1).reshape(-1), cache.slots(seq, ctx), 1, cache)
+    plain = model.forward(*args).float()
+    fused = model.forward(*args, fused_decode=True).float()
+    torch.testing.assert_close(fused, plain, rtol=2e-2, atol=2e-3)

@@ -18,6 +18,7 @@ from pagedbatch_amd import sampling as smp
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "pbsample.h")
+ATTN_HEADER = os.path.join(ROOT, "include", "pbattn.h")
 
 
 # ---------------------------------------------------------------- SamplingParams mirror
@@ -103,18 +104,20 @@ def test_status_mapping():
 
 
 # ---------------------------------------------------------------- the C ABI library
-def _header_functions() -> list[str]:
-    text = open(HEADER).read()
+def _header_functions(path: str = HEADER) -> list[str]:
+    text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"\b(pbs_\w+)\s*\(", text)
+    return re.findall(r"\b(pb[sa]_\w+)\s*\(", text)
 
 
 def test_library_exports_every_header_symbol():
     lib = _lib.load()
     names = _header_functions()
     assert set(names) == set(_lib.SYMBOLS), (names, _lib.SYMBOLS)
+    attn = _header_functions(ATTN_HEADER)
+    assert set(attn) == set(_lib.ATTN_SYMBOLS), (attn, _lib.ATTN_SYMBOLS)
     raw = ctypes.CDLL(_lib.LIB_PATH)
-    for n in names:
+    for n in names + attn:
         assert hasattr(raw, n), n
     assert lib.pbs_abi_version() == _lib.ABI_VERSION
     m = re.search(r"#define PBS_ABI_VERSION (\d+)", open(HEADER).read())
@@ -201,3 +204,31 @@ def test_paged_kv_slots_are_distinct_and_blocked():
     assert int(s.max()) < kv.k[0].shape[0]
     # within a block the slots are consecutive
     assert torch.equal(s[:, 1:8] - s[:, :7], torch.ones(5, 7, dtype=s.dtype))
+
+
+def _attn(lib, **kw):
+    a = dict(q=1 << 20, k=1 << 20, v=1 << 20, n_slots=64, bt=1 << 20, max_blocks=4, lens=1 << 20, rows=2, hq=9, hkv=3,
+             d=64, bs=16, maxc=64, out=1 << 20)
+    a.update(kw)
+    return lib.pba_decode_attention(a["q"], a["k"], a["v"], a["n_slots"], a["bt"], a["max_blocks"], a["lens"], a["rows"],
+                                    a["hq"], a["hkv"], a["d"], a["bs"], a["maxc"], 0.125, a["out"], None)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    ({"rows": -1}, "negative"),
+    ({"q": None}, "null"),
+    ({"d": 128}, "head_dim"),
+    ({"hq": 10}, "multiple"),
+    ({"hq": 27}, "at most 8"),
+    ({"maxc": 65}, "max_context"),
+    ({"maxc": 5000, "max_blocks": 400}, "max_context"),
+    ({"bs": 0}, "block_size"),
+])
+def test_attention_abi_rejects_bad_arguments(kw, msg):
+    lib = _lib.load()
+    assert _attn(lib, **kw) == _lib.ERR_INVALID_ARGUMENT
+    assert msg in _lib.last_error(lib)
+
+
+def test_attention_abi_zero_rows_is_a_no_op():
+    assert _attn(_lib.load(), rows=0) == _lib.OK
