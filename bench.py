@@ -119,8 +119,9 @@ def cpu_baseline(w, steps: int, rows: int):
 
 def engine_step(args):
     """The end-to-end engine step (smollm2-135m-random, 64 requests x 128 prompt + 128
-    output tokens, half greedy, half top-k=50 / top-p=0.9): decode throughput and the
-    sampler's share of the step, with the batched call and with one call per row."""
+    output tokens, half greedy, half top-k=50 / top-p=0.9): decode throughput (`value`:
+    batched sampling and the paged-attention decode kernel) and the sampler's share of
+    the step, with the batched call and with one call per row (torch attention)."""
     import torch
 
     from pagedbatch_amd import engine_step as es
@@ -134,6 +135,11 @@ def engine_step(args):
     print("[bench] engine step: one sampling call per row", file=sys.stderr, flush=True)
     tr, out_r = es.run(shape, **kw, per_row=True)
     same = out_b == out_r
+    print("[bench] engine step: batched sampling, paged-attention decode kernel", file=sys.stderr, flush=True)
+    tf, out_f = es.run(shape, **kw, fused_decode=True)
+    # the fused attention rounds differently in the last fp32 bits, which the bf16 o_proj
+    # input can turn into different tokens later in a sequence: report the agreement
+    agree = sum(a == b for x, y in zip(out_b, out_f) for a, b in zip(x, y)) / sum(len(x) for x in out_b)
 
     def split(t):
         fwd, smp = t.forward_s[1:], t.sample_s[1:]  # decode steps (step 0 is the prefill)
@@ -143,8 +149,8 @@ def engine_step(args):
                 "sample_share": round(sum(smp) / (sum(fwd) + sum(smp)), 4),
                 "prefill_forward_ms": round(1e3 * t.forward_s[0], 3), "prefill_sample_ms": round(1e3 * t.sample_s[0], 4)}
 
-    b, r = split(tb), split(tr)
-    step_ms = b["forward_ms"] + b["sample_ms"]
+    b, r, f = split(tb), split(tr), split(tf)
+    step_ms = f["forward_ms"] + f["sample_ms"]
 
     # the step's stop check (engine.py:173-182) for its 64 rows on the device: one kernel
     # from device tokens and one copy back, timed from launch to the reasons on the host
@@ -169,8 +175,10 @@ def engine_step(args):
         "warmup": 1, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights, random prompt ids)",
         "config": {"workload": "engine_step_smollm2", "requests": 64, "prompt_len": 128, "output_len": 128,
-                   "block_size": 16, "mix": "half greedy, half top_k=50 top_p=0.9 T=1.0"},
-        "batched_sampling": b, "per_row_sampling": r, "same_tokens_batched_vs_per_row": same,
+                   "block_size": 16, "mix": "half greedy, half top_k=50 top_p=0.9 T=1.0",
+                   "decode_attention": "paged-attention kernel (pba_decode_attention)"},
+        "fused_decode_attention": f, "batched_sampling": b, "per_row_sampling": r,
+        "same_tokens_batched_vs_per_row": same, "token_agreement_fused_vs_torch_attention": round(agree, 4),
         "finish_check_us": round(1e6 * sorted(fin[5:])[len(fin[5:]) // 2], 1),
         "torch": torch.__version__,
     }

@@ -9,8 +9,9 @@
 //      (pagedbatch/block_manager.py:88-91), the K row (64 bf16, eight 16-byte loads) and
 //      the n_rep scaled dot products, in fp32, into an LDS score table.
 //   2. Per query head: the maximum and the sum of exp(score - max) (block reductions).
-//   3. Thread (head, dim) pairs accumulate sum_t p[t] * V[t][dim]: for a given t the 64
-//      threads of a head read one contiguous 128-byte V row.
+//   3. V rows in tiles of 256 positions staged through LDS (eight independent 16-byte
+//      loads per thread), then threads (position group, dim) accumulate
+//      sum_t p[t] * V[t][dim] for every query head.
 // Memory: (K + V) * context * 128 B per (sequence, KV head), read once; HBM-bound for
 // long contexts, launch- and latency-bound for short ones.
 
@@ -29,7 +30,7 @@ namespace pba {
 constexpr int NT = 256;
 constexpr int D = 64;
 constexpr int MAX_REP = 8;
-constexpr int MAX_CONTEXT = 4096;
+constexpr int MAX_CONTEXT = 2048;
 
 struct Args {
   const float* q;
@@ -64,9 +65,11 @@ __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) 
 
 __global__ __launch_bounds__(NT) void k_decode(Args a) {
   extern __shared__ float lds[];
-  float* qs = lds;                                   // [rep][D]
+  uint4* vt = (uint4*)lds;                           // [NT][D / 8]: a tile of V rows
+  float* qs = (float*)(vt + NT * (D / 8));           // [rep][D]
   float* red = qs + MAX_REP * D;                     // [NT / 64]
-  int* slot_s = (int*)(red + NT / 64);               // [max_context]
+  float* part = red + NT / 64;                       // [NT / D][MAX_REP][D] partial sums
+  int* slot_s = (int*)(part + (NT / D) * MAX_REP * D);  // [max_context]
   float* sc = (float*)(slot_s + a.max_context);      // [rep][max_context]
 
   const int b = blockIdx.x / a.n_kv_heads;
@@ -144,18 +147,43 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
   }
   __syncthreads();
 
-  // 3. weighted sum of the V rows: thread pairs (head, dim)
-  for (int p = tid; p < rep * D; p += NT) {
-    const int h = p / D, d = p % D;
-    const float* w = sc + h * a.max_context;
-    float acc = 0.0f;
-    for (int t = 0; t < L; ++t) {
-      const uint16_t raw = a.v[((size_t)slot_s[t] * a.n_kv_heads + kvh) * D + d];
-      acc = fmaf(w[t], __uint_as_float((uint32_t)raw << 16), acc);
+  // 3. weighted sum of the V rows, in tiles of NT positions staged through LDS (every
+  //    thread issues its eight 16-byte loads of a tile at once); thread (q4, d) then takes
+  //    dim d and the tile's positions q4, q4 + 4, ... for every query head (one V element
+  //    read serves them all); the four position groups' partial sums meet in LDS
+  const int d = tid & (D - 1), q4 = tid >> 6;
+  float acc[MAX_REP];
+#pragma unroll
+  for (int h = 0; h < MAX_REP; ++h) acc[h] = 0.0f;
+  for (int t0 = 0; t0 < L; t0 += NT) {
+    const int n = min(NT, L - t0);
+    __syncthreads();  // the previous tile is consumed
+#pragma unroll
+    for (int i0 = 0; i0 < NT * (D / 8); i0 += NT) {
+      const int i = i0 + tid, r = i >> 3;
+      if (r < n) vt[i] = ((const uint4*)(a.v + ((size_t)slot_s[t0 + r] * a.n_kv_heads + kvh) * D))[i & 7];
     }
-    float s = 0.0f;
+    __syncthreads();
+    for (int r = q4; r < n; r += NT / D) {
+      const float vv = __uint_as_float((uint32_t)((const uint16_t*)(vt + r * (D / 8)))[d] << 16);
+#pragma unroll
+      for (int h = 0; h < MAX_REP; ++h)
+        if (h < rep) acc[h] = fmaf(sc[h * a.max_context + t0 + r], vv, acc[h]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < MAX_REP; ++h)
+    if (h < rep) part[(q4 * MAX_REP + h) * D + d] = acc[h];
+  __syncthreads();
+  for (int p = tid; p < rep * D; p += NT) {
+    const int h = p / D, dd = p % D;
+    float tot = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NT / D; ++g) tot += part[(g * MAX_REP + h) * D + dd];
+    float s = 1.0f;
+#pragma unroll
     for (int hh = 0; hh < MAX_REP; ++hh) s = (hh == h) ? sum[hh] : s;
-    out[p] = acc / s;
+    out[p] = tot / s;
   }
 }
 
@@ -178,7 +206,7 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "block_size, max_blocks and n_slots must be positive");
   if (max_context < 1 || max_context > MAX_CONTEXT || (int64_t)max_context > max_blocks * block_size)
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT,
-                             "max_context must be in [1, 4096] and covered by max_blocks * block_size");
+                             "max_context must be in [1, 2048] and covered by max_blocks * block_size");
   if (rows * n_kv_heads > 0x7fffffff) return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "too many rows");
   Args a;
   a.q = q;
@@ -195,8 +223,8 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
   a.max_context = max_context;
   a.scale = scale;
   a.out = out;
-  const size_t lds = sizeof(float) * (MAX_REP * D + NT / 64) + sizeof(int) * max_context +
-                     sizeof(float) * (size_t)a.rep * max_context;
+  const size_t lds = sizeof(uint4) * NT * (D / 8) + sizeof(float) * (MAX_REP * D + NT / 64 + (NT / D) * MAX_REP * D) +
+                     sizeof(int) * max_context + sizeof(float) * (size_t)a.rep * max_context;
   if (lds > 64 * 1024) {
     const hipError_t ea = hipFuncSetAttribute((const void*)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (ea != hipSuccess) return pbs::report_error(PBS_ERR_HIP, hipGetErrorString(ea));
