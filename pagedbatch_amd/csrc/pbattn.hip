@@ -48,27 +48,38 @@ struct Args {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
-  // wave reduction by shuffles, then the 4 wave results through LDS
-  for (int off = 32; off > 0; off >>= 1) {
-    const float o = __shfl_xor(v, off, 64);
-    v = is_max ? fmaxf(v, o) : v + o;
+// N values at once, max or sum over the workgroup: shuffles inside each wave, then the
+// waves' results through LDS (red: [NT / 64][N]); every thread gets the totals
+template <bool MAX, int N>
+__device__ __forceinline__ void block_reduce_n(float (&v)[N], float* red) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    for (int off = 32; off > 0; off >>= 1) {
+      const float o = __shfl_xor(v[i], off, 64);
+      v[i] = MAX ? fmaxf(v[i], o) : v[i] + o;
+    }
   }
   const int w = threadIdx.x >> 6;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) red[w * N + i] = v[i];
+  }
   __syncthreads();
-  float r = red[0];
-  for (int i = 1; i < NT / 64; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
-  return r;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float r = red[i];
+    for (int ww = 1; ww < NT / 64; ++ww) r = MAX ? fmaxf(r, red[ww * N + i]) : r + red[ww * N + i];
+    v[i] = r;
+  }
 }
 
 __global__ __launch_bounds__(NT) void k_decode(Args a) {
   extern __shared__ float lds[];
   uint4* vt = (uint4*)lds;                           // [NT][D / 8]: a tile of V rows
   float* qs = (float*)(vt + NT * (D / 8));           // [rep][D]
-  float* red = qs + MAX_REP * D;                     // [NT / 64]
-  float* part = red + NT / 64;                       // [NT / D][MAX_REP][D] partial sums
+  float* red = qs + MAX_REP * D;                     // [NT / 64][MAX_REP + 1]
+  float* part = red + (NT / 64) * (MAX_REP + 1);     // [NT / D][MAX_REP][D] partial sums
   int* slot_s = (int*)(part + (NT / D) * MAX_REP * D);  // [max_context]
   float* sc = (float*)(slot_s + a.max_context);      // [rep][max_context]
 
@@ -124,28 +135,31 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
       }
     }
   }
-  // a corrupt slot anywhere in the context: this sequence's output is NaN
-  bad = (int)block_reduce((float)bad, red, true);
-  if (bad) {
+  // 2. one block reduction for every head's maximum and the corrupt-slot flag, one for
+  //    every head's sum of exponentials (the weights replace the scores in place)
+  float mv[MAX_REP + 1];
+#pragma unroll
+  for (int h = 0; h < MAX_REP; ++h) mv[h] = mx[h];
+  mv[MAX_REP] = bad ? 1.0f : 0.0f;
+  block_reduce_n<true>(mv, red);
+  if (mv[MAX_REP] > 0.0f) {  // a corrupt slot anywhere in the context: NaN out
     for (int i = tid; i < rep * D; i += NT) out[i] = __int_as_float(0x7fc00000);
     return;
   }
-
-  // 2. softmax weights per head (in place) and their sums
-  float sum[MAX_REP];
+  float sum[MAX_REP + 1];
 #pragma unroll
-  for (int h = 0; h < MAX_REP; ++h) sum[h] = 1.0f;
-  for (int h = 0; h < rep; ++h) {
-    const float m = block_reduce(mx[h], red, true);
-    float s = 0.0f;
-    for (int t = tid; t < L; t += NT) {
-      const float e = __expf(sc[h * a.max_context + t] - m);
-      sc[h * a.max_context + t] = e;
-      s += e;
+  for (int h = 0; h <= MAX_REP; ++h) sum[h] = 0.0f;
+  for (int t = tid; t < L; t += NT) {
+#pragma unroll
+    for (int h = 0; h < MAX_REP; ++h) {
+      if (h < rep) {
+        const float e = __expf(sc[h * a.max_context + t] - mv[h]);
+        sc[h * a.max_context + t] = e;
+        sum[h] += e;
+      }
     }
-    sum[h] = block_reduce(s, red, false);
   }
-  __syncthreads();
+  block_reduce_n<false>(sum, red);
 
   // 3. weighted sum of the V rows, in tiles of NT positions staged through LDS (every
   //    thread issues its eight 16-byte loads of a tile at once); thread (q4, d) then takes
@@ -223,7 +237,8 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
   a.max_context = max_context;
   a.scale = scale;
   a.out = out;
-  const size_t lds = sizeof(uint4) * NT * (D / 8) + sizeof(float) * (MAX_REP * D + NT / 64 + (NT / D) * MAX_REP * D) +
+  const size_t lds = sizeof(uint4) * NT * (D / 8) +
+                     sizeof(float) * (MAX_REP * D + (NT / 64) * (MAX_REP + 1) + (NT / D) * MAX_REP * D) +
                      sizeof(int) * max_context + sizeof(float) * (size_t)a.rep * max_context;
   if (lds > 64 * 1024) {
     const hipError_t ea = hipFuncSetAttribute((const void*)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
