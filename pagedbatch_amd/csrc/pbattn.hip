@@ -222,6 +222,8 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT,
                              "max_context must be in [1, 2048] and covered by max_blocks * block_size");
   if (rows * n_kv_heads > 0x7fffffff) return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "too many rows");
+  if (n_slots > 0x7fffffff)  // slot numbers are kept as 32-bit ints in LDS
+    return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "n_slots must be below 2^31");
   Args a;
   a.q = q;
   a.k = k_cache;

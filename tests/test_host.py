@@ -223,6 +223,7 @@ def _attn(lib, **kw):
     ({"maxc": 65}, "max_context"),
     ({"maxc": 5000, "max_blocks": 400}, "max_context"),
     ({"bs": 0}, "block_size"),
+    ({"n_slots": 1 << 31}, "n_slots"),
 ])
 def test_attention_abi_rejects_bad_arguments(kw, msg):
     lib = _lib.load()
