@@ -16,7 +16,7 @@ rocprofv3 kernel trace reports). Each launch is also timed on its own with an ev
 ``--workload engine_step_smollm2`` instead runs the end-to-end engine step
 (pagedbatch_amd/engine_step.py) and reports decode tokens/s and the sampler's share.
 
-Prints one JSON line (rank 0): metric/value/unit as BASELINE.json names them, plus a
+Prints one JSON line (rank 0): the workload's metric with its value and unit, plus a
 ``roofline`` object for the sampling kernel and a ``cpu_baseline`` object (the op-for-op
 CPU restatement of pagedbatch/sampling.py timed on this host in the same run).
 """

@@ -1,7 +1,7 @@
 """Parity comparison of sampler outputs against the oracle -- TEST INFRASTRUCTURE ONLY.
 
 Used by tests/, ``__graft_entry__.smoke()`` and bench.py to check kernel results. The
-bar, applied row by row:
+bar for the sampler, applied row by row:
 
 * greedy rows: token bit-exact (lowest-index ties, first NaN);
 * error statuses identical;
