@@ -1,6 +1,6 @@
 """CPU oracle for the finish-reason check -- TEST INFRASTRUCTURE ONLY.
 
-Nothing in the product imports this module: only ``tests/`` use it, as the checker of
+Nothing in the product imports this module: only ``tests/`` use it, to hold the expected results of
 ``pbs_finish_reasons`` (``pagedbatch_amd/finish.py``), which runs on the GPU and fails
 loudly when the library is missing.
 

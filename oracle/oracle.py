@@ -2,7 +2,7 @@
 
 Nothing in the product imports this module: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg use it, and
-only as the checker. The product path (``pagedbatch_amd``) runs the HIP
+only for expected results and the CPU timing. The product path (``pagedbatch_amd``) runs the HIP
 kernels and fails loudly when they are missing.
 
 It restates ``pagedbatch/sampling.py:10-27`` row by row in numpy, in float64
