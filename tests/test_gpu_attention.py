@@ -31,7 +31,7 @@ def _torch_decode(q, kc, vc, block_table, lens, block_size, scale):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed", [(4, 9, 3, 16, 200, 1), (3, 8, 8, 8, 37, 2), (2, 16, 2, 32, 1500, 3),
-                                                   (5, 4, 1, 16, 1, 4)])
+                                                   (5, 4, 1, 16, 1, 4), (2, 16, 2, 16, 2048, 5)])
 def test_decode_matches_torch(B, Hq, Hkv, bs, maxL, seed):
     from pagedbatch_amd.attention import decode_attention
 
