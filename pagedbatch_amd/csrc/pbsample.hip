@@ -30,6 +30,52 @@
 
 #include "pbsample.h"
 
+// Translation units. The library is built from several compilations of this file so that
+// they run in parallel: PBS_TU_DTYPE=n compiles the kernels of one logits type and
+// launch_dt<n>; PBS_TU_ABI compiles the C ABI and the finish kernel. Without either macro
+// the file is the whole library in one unit.
+#if defined(PBS_TU_DTYPE)
+#define PBS_WANT_KERNELS 1
+#define PBS_WANT_ABI 0
+#elif defined(PBS_TU_ABI)
+#define PBS_WANT_KERNELS 0
+#define PBS_WANT_ABI 1
+#else
+#define PBS_WANT_KERNELS 1
+#define PBS_WANT_ABI 1
+#endif
+
+namespace pbs {
+
+struct KArgs {
+  const void* logits;
+  int64_t n_logit_rows;
+  int64_t row_stride;  // elements
+  int vocab;
+  int nvec;            // 16-byte vectors per row (vector sources), ceil(vocab/EPV) otherwise
+  const int32_t* row_map;
+  const float* temperature;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* uniform;
+  int32_t* out_token;
+  int32_t* out_status;
+  float* out_probs;
+  uint8_t* out_kept;
+  pbs_row_info* out_info;
+};
+
+// one launch of the sampler for logits type DT (defined with the kernels)
+template <int DT>
+int launch_dt(const KArgs& a, int64_t rows, bool vec, hipStream_t stream);
+
+// error reporting shared by the translation units (pbs_last_error reads it)
+int report_error(int code, const char* msg);
+int report_errorf(int code, const char* fmt, ...);
+
+}  // namespace pbs
+
+#if PBS_WANT_KERNELS
 namespace pbs {
 
 constexpr int NT = 512;            // threads per workgroup: one workgroup per row
@@ -368,23 +414,6 @@ struct UnitDivider {
 // ---------------------------------------------------------------------------------------
 // kernel arguments and per-row shared state
 // ---------------------------------------------------------------------------------------
-struct KArgs {
-  const void* logits;
-  int64_t n_logit_rows;
-  int64_t row_stride;  // elements
-  int vocab;
-  int nvec;            // 16-byte vectors per row (vector sources), ceil(vocab/EPV) otherwise
-  const int32_t* row_map;
-  const float* temperature;
-  const int32_t* top_k;
-  const float* top_p;
-  const float* uniform;
-  int32_t* out_token;
-  int32_t* out_status;
-  float* out_probs;
-  uint8_t* out_kept;
-  pbs_row_info* out_info;
-};
 
 struct RowState {
   int status;
@@ -2858,6 +2887,42 @@ __global__ __launch_bounds__(NT) void k_sample(KArgs a) {
   }
 }
 
+template <int DT>
+int launch_dt(const KArgs& a, int64_t rows, bool vec, hipStream_t stream) {
+  const dim3 grid((unsigned)rows), block(NT);
+  if (!vec) {
+    hipLaunchKernelGGL((k_sample<DT, -1>), grid, block, 0, stream, a);
+  } else {
+    const int nch = (a.nvec + NT - 1) / NT;
+    if (nch <= 1) hipLaunchKernelGGL((k_sample<DT, 1>), grid, block, 0, stream, a);
+    else if (nch <= 2) hipLaunchKernelGGL((k_sample<DT, 2>), grid, block, 0, stream, a);
+    else if (nch <= 4) hipLaunchKernelGGL((k_sample<DT, 4>), grid, block, 0, stream, a);
+    else if (nch <= 8) hipLaunchKernelGGL((k_sample<DT, 8>), grid, block, 0, stream, a);
+    else if (nch <= 12) hipLaunchKernelGGL((k_sample<DT, 12>), grid, block, 0, stream, a);
+    else if (nch <= 16) hipLaunchKernelGGL((k_sample<DT, 16>), grid, block, 0, stream, a);
+    else if (nch <= 24) hipLaunchKernelGGL((k_sample<DT, 24>), grid, block, 0, stream, a);
+    else if (nch <= 32) hipLaunchKernelGGL((k_sample<DT, 32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((k_sample<DT, 0>), grid, block, 0, stream, a);
+  }
+  if (a.out_probs || a.out_kept) {
+    if (vec) hipLaunchKernelGGL((k_debug<DT, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((k_debug<DT, false>), grid, block, 0, stream, a);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return report_errorf(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return PBS_OK;
+}
+
+}  // namespace pbs
+
+#if defined(PBS_TU_DTYPE)
+template int pbs::launch_dt<PBS_TU_DTYPE>(const pbs::KArgs&, int64_t, bool, hipStream_t);
+#endif
+#endif  // PBS_WANT_KERNELS
+
+#if PBS_WANT_ABI
+namespace pbs {
+
 // ---------------------------------------------------------------------------------------
 // Finish reasons after a step's tokens (pagedbatch/engine.py:173-182): one thread per
 // sequence, reading the token the sampler wrote and the sequence's stop rule.
@@ -2908,33 +2973,6 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-template <int DT>
-int launch_dt(const pbs::KArgs& a, int64_t rows, bool vec, hipStream_t stream) {
-  using namespace pbs;
-  const dim3 grid((unsigned)rows), block(NT);
-  if (!vec) {
-    hipLaunchKernelGGL((k_sample<DT, -1>), grid, block, 0, stream, a);
-  } else {
-    const int nch = (a.nvec + NT - 1) / NT;
-    if (nch <= 1) hipLaunchKernelGGL((k_sample<DT, 1>), grid, block, 0, stream, a);
-    else if (nch <= 2) hipLaunchKernelGGL((k_sample<DT, 2>), grid, block, 0, stream, a);
-    else if (nch <= 4) hipLaunchKernelGGL((k_sample<DT, 4>), grid, block, 0, stream, a);
-    else if (nch <= 8) hipLaunchKernelGGL((k_sample<DT, 8>), grid, block, 0, stream, a);
-    else if (nch <= 12) hipLaunchKernelGGL((k_sample<DT, 12>), grid, block, 0, stream, a);
-    else if (nch <= 16) hipLaunchKernelGGL((k_sample<DT, 16>), grid, block, 0, stream, a);
-    else if (nch <= 24) hipLaunchKernelGGL((k_sample<DT, 24>), grid, block, 0, stream, a);
-    else if (nch <= 32) hipLaunchKernelGGL((k_sample<DT, 32>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((k_sample<DT, 0>), grid, block, 0, stream, a);
-  }
-  if (a.out_probs || a.out_kept) {
-    if (vec) hipLaunchKernelGGL((k_debug<DT, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((k_debug<DT, false>), grid, block, 0, stream, a);
-  }
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-  return PBS_OK;
-}
-
 int sample_impl(const void* logits, int dtype, int64_t n_logit_rows, int64_t rows, int64_t vocab,
                 int64_t row_stride, const int32_t* row_map, const float* temperature, const int32_t* top_k,
                 const float* top_p, const float* uniform, int32_t* out_token, int32_t* out_status,
@@ -2977,17 +3015,23 @@ int sample_impl(const void* logits, int dtype, int64_t n_logit_rows, int64_t row
   a.out_info = out_info;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case PBS_DTYPE_F32: return launch_dt<PBS_DTYPE_F32>(a, rows, vec, st);
-    case PBS_DTYPE_F16: return launch_dt<PBS_DTYPE_F16>(a, rows, vec, st);
-    default: return launch_dt<PBS_DTYPE_BF16>(a, rows, vec, st);
+    case PBS_DTYPE_F32: return pbs::launch_dt<PBS_DTYPE_F32>(a, rows, vec, st);
+    case PBS_DTYPE_F16: return pbs::launch_dt<PBS_DTYPE_F16>(a, rows, vec, st);
+    default: return pbs::launch_dt<PBS_DTYPE_BF16>(a, rows, vec, st);
   }
 }
 
 }  // namespace
 
 namespace pbs {
-// error reporting for the library's other translation units (pbs_last_error reads it)
 int report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+int report_errorf(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
 }  // namespace pbs
 
 extern "C" {
@@ -3053,3 +3097,5 @@ int pbs_finish_reasons(const int32_t* tokens, int64_t rows, int32_t eos_token_id
 }
 
 }  // extern "C"
+
+#endif  // PBS_WANT_ABI
