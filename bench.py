@@ -11,7 +11,9 @@ The K timed steps are one replay of a HIP graph holding the K launches (``value`
 average duration (``us_per_step_kernel``, the roofline's time base, the figure the
 rocprofv3 kernel trace reports). Each launch is also timed on its own with an event pair
 (``us_per_launch_events``, which also spans the launch's dispatch), and the Python
-``sample()`` surface per step is reported as ``us_per_step_python``.
+``sample()`` surface per step is reported as ``us_per_step_python`` (256 seeded
+generators) with its split into uniforms, packing and launch + copy back + sync for one
+shared generator and for 256 seeded ones (``python_surface``).
 
 ``--workload engine_step_smollm2`` instead runs the end-to-end engine step
 (pagedbatch_amd/engine_step.py) and reports decode tokens/s and the sampler's share.
@@ -117,6 +119,103 @@ def cpu_baseline(w, steps: int, rows: int):
     }
 
 
+def source_sha() -> str:
+    """sha256 (first 16 hex digits) of the sampler kernel source the library is built from."""
+    import hashlib
+
+    with open(os.path.join(ROOT, "pagedbatch_amd", "csrc", "pbsample.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def committed_traffic(workload: str):
+    """HBM bytes per launch from the committed counter profile
+    (profiles/traffic_<workload>.json, written from two rocprofv3 --pmc runs), reported only
+    when that profile was measured on the kernel source this library is built from."""
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    if not os.path.exists(tpath):
+        return None, "no committed counter profile for this workload"
+    with open(tpath) as f:
+        prof = json.load(f)
+    sha = source_sha()
+    if prof.get("source_sha") != sha:
+        return None, (f"profiles/traffic_{workload}.json was measured on kernel source "
+                      f"{prof.get('source_sha')}, this build is {sha}: not reported")
+    return prof.get("hbm_bytes_per_launch"), (f"profiles/traffic_{workload}.json (rocprofv3 FETCH_SIZE + "
+                                               f"WRITE_SIZE, calibrated on a copy kernel; kernel source {sha})")
+
+
+def python_surface(w, bufs, copies, rows):
+    """The whole Python ``sample()`` surface per engine step, median of 20 calls, split into
+    the uniforms (one torch.rand per run of rows sharing a generator), packing the
+    parameters into the pinned staging block, and the launch plus the copy back and the
+    synchronisation; once with one shared generator (the engine's, engine.py:58) and once
+    with a seeded generator per row (every request seeded, engine.py:84)."""
+    import torch
+
+    from pagedbatch_amd import SamplingParams
+    from pagedbatch_amd.sampling import _sample
+
+    sp = [SamplingParams(temperature=w.temperature[i], top_k=w.top_k[i], top_p=w.top_p[i]) for i in range(rows)]
+    out = {}
+    for name in ("shared_generator", "seeded_generators"):
+        shared = torch.Generator().manual_seed(0)
+        gens = [shared] * rows if name == "shared_generator" else [torch.Generator().manual_seed(i)
+                                                                 for i in range(rows)]
+        for i in range(3):
+            _sample(bufs[i % copies], sp, gens, None)
+        parts = {"uniforms_us": [], "pack_us": [], "launch_sync_us": [], "total_us": []}
+        for i in range(20):
+            tm = {}
+            t0 = time.perf_counter()
+            _sample(bufs[i % copies], sp, gens, None, timing=tm)
+            t1 = time.perf_counter()
+            parts["uniforms_us"].append(tm["uniforms"] - tm["start"])
+            parts["pack_us"].append(tm["pack"] - tm["uniforms"])
+            parts["launch_sync_us"].append(tm["launch_sync"] - tm["pack"])
+            parts["total_us"].append(t1 - t0)
+        out[name] = {k: round(statistics.median(v) * 1e6, 1) for k, v in parts.items()}
+    return out
+
+
+def engine_sampler_kernel_us(cap) -> float:
+    """The sampling kernel alone on one decode step's logits (bf16 [64, 49152], the step's
+    own parameters and uniforms): mean of 50 back-to-back launches between HIP events on
+    the launch stream."""
+    import torch
+
+    from pagedbatch_amd import _lib
+    from pagedbatch_amd.sampling import _TORCH_DTYPE
+
+    dev = cap.logits.device
+    lib = _lib.load()
+    rows, vocab = cap.logits.shape
+    T = torch.tensor(cap.temperature, dtype=torch.float32, device=dev)
+    K = torch.tensor([k if 0 < k < vocab else 0 for k in cap.top_k], dtype=torch.int32, device=dev)
+    P = torch.tensor(cap.top_p, dtype=torch.float32, device=dev)
+    U = torch.tensor(cap.uniform, dtype=torch.float32, device=dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch():
+        rc = lib.pbs_sample(cap.logits.data_ptr(), _TORCH_DTYPE[cap.logits.dtype], rows, rows, vocab, vocab, None,
+                            T.data_ptr(), K.data_ptr(), P.data_ptr(), U.data_ptr(), tok.data_ptr(), st.data_ptr(),
+                            None, 0, stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(_lib.last_error(lib))
+
+    for _ in range(5):
+        launch()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(50):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    assert tok.cpu().tolist() == cap.tokens
+    return round(e0.elapsed_time(e1) * 1e3 / 50, 3)
+
+
 def engine_step(args):
     """The end-to-end engine step (smollm2-135m-random, 64 requests x 128 prompt + 128
     output tokens, half greedy, half top-k=50 / top-p=0.9): decode throughput (`value`:
@@ -136,7 +235,8 @@ def engine_step(args):
     tr, out_r = es.run(shape, **kw, per_row=True)
     same = out_b == out_r
     print("[bench] engine step: batched sampling, paged-attention decode kernel", file=sys.stderr, flush=True)
-    tf, out_f = es.run(shape, **kw, fused_decode=True)
+    tf, out_f = es.run(shape, **kw, fused_decode=True, capture_steps=(kw["output_len"] - 1,))
+    sampler_kernel_us = engine_sampler_kernel_us(tf.captures[0])
     # the fused attention rounds differently in the last fp32 bits, which the bf16 o_proj
     # input can turn into different tokens later in a sequence: report the agreement
     agree = sum(a == b for x, y in zip(out_b, out_f) for a, b in zip(x, y)) / sum(len(x) for x in out_b)
@@ -151,24 +251,10 @@ def engine_step(args):
 
     b, r, f = split(tb), split(tr), split(tf)
     step_ms = f["forward_ms"] + f["sample_ms"]
-
-    # the step's stop check (engine.py:173-182) for its 64 rows on the device: one kernel
-    # from device tokens and one copy back, timed from launch to the reasons on the host
-    import time
-
-    from pagedbatch_amd.finish import FinishRule, finish_codes
-
-    dev = torch.device("cuda", 0)
-    toks = torch.tensor([o[-1] for o in out_b], dtype=torch.int32, device=dev)
-    rules = [FinishRule(ignore_eos=False, stop_token_ids=(), num_output=128, max_tokens=128, num_tokens=256)
-             for _ in out_b]
-    fin = []
-    for i in range(25):
-        torch.cuda.synchronize(dev)
-        t0 = time.perf_counter()
-        codes = finish_codes(toks, rules, None, 2048).cpu()
-        fin.append(time.perf_counter() - t0)
-    assert (codes == 2).all()  # every request has its 128 outputs: "length"
+    # the batched call runs the stop check (engine.py:173-182) on the device after the
+    # sampler and brings the reasons back with the tokens: every request ends on "length"
+    # at its 128th output, none before
+    assert tb.reasons[-1] == ["length"] * 64 and all(x is None for rs in tb.reasons[:-1] for x in rs)
     line = {
         "metric": "engine decode tokens/s (smollm2-135m-random bf16, 64 requests, 128 prompt + 128 output tokens)",
         "value": round(64 / (step_ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": b["decode_steps"],
@@ -179,7 +265,8 @@ def engine_step(args):
                    "decode_attention": "paged-attention kernel (pba_decode_attention)"},
         "fused_decode_attention": f, "batched_sampling": b, "per_row_sampling": r,
         "same_tokens_batched_vs_per_row": same, "token_agreement_fused_vs_torch_attention": round(agree, 4),
-        "finish_check_us": round(1e6 * sorted(fin[5:])[len(fin[5:]) // 2], 1),
+        "stop_check": "on the device after the sampler, reasons in the tokens' copy back (in sample_ms)",
+        "sampler_kernel_us": sampler_kernel_us,
         "torch": torch.__version__,
     }
     print(json.dumps(line), flush=True)
@@ -295,27 +382,8 @@ def main():
         rep = compare_rows(tokens[:n], status[:n], refs, [t == 0 for t in w.temperature[:n]])
         parity = {"rows": n, "ok": rep.ok(), "tokens_checked": rep.checked_tokens, "exempt": rep.exempt_tokens}
 
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.workload}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-
-    # the whole Python surface per engine step: parameter packing, one uniform per
-    # stochastic row from its seeded generator, H2D of the packed parameters, the launch,
-    # D2H of tokens and statuses, and the synchronisation (pagedbatch_amd.sample)
-    from pagedbatch_amd import SamplingParams, sample
-
-    sp = [SamplingParams(temperature=w.temperature[i], top_k=w.top_k[i], top_p=w.top_p[i]) for i in range(rows)]
-    gens = [torch.Generator().manual_seed(i) for i in range(rows)]
-    for i in range(3):
-        sample(bufs[i % copies], sp, gens)
-    e2e = []
-    for i in range(20):
-        t0 = time.perf_counter()
-        sample(bufs[i % copies], sp, gens)
-        e2e.append(time.perf_counter() - t0)
-    e2e_us = statistics.median(e2e) * 1e6
+    traffic, traffic_note = committed_traffic(args.workload)
+    surface = python_surface(w, bufs, copies, rows)
 
     cpu = None
     if not args.no_cpu:
@@ -333,7 +401,8 @@ def main():
         "us_per_step_kernel": round(replay_kern_ms * 1e3, 3),
         "us_per_launch_events": round(kern_ms * 1e3, 3),
         "ms_per_step_eager_launches": round(eager_ms, 5),
-        "us_per_step_python": round(e2e_us, 1),
+        "us_per_step_python": surface["seeded_generators"]["total_us"],
+        "python_surface": surface,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -343,7 +412,7 @@ def main():
                    "buffers_rotated": copies, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": alg_bytes},
+                     "traffic_source": traffic_note, "algorithmic_bytes_per_launch": alg_bytes},
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
         "parity": parity,

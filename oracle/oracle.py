@@ -43,6 +43,9 @@ ROW_BAD_PARAM = 3
 
 DTYPES = ("float32", "float16", "bfloat16")
 
+# sampling-order positions kept on each side of the cutoff in RowResult.cut_window
+WINDOW = 256
+
 
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
     """bfloat16 bit patterns (uint16) -> float32, exact."""
@@ -89,6 +92,13 @@ class RowResult:
     cut_margin: float = float("inf")
     kept: np.ndarray | None = field(default=None, repr=False)
     probs: np.ndarray | None = field(default=None, repr=False)
+    # the sampling order (value descending, index ascending over the top-k set) near the
+    # cutoff and near the draw, for checking rows inside the 1e-6 bands:
+    #   cut_window  (first position, indices, exclusive mass / Z_K) around the kept count
+    #   draw_window (first position, indices, exclusive and inclusive mass / Z_P) around
+    #               the drawn position
+    cut_window: tuple | None = field(default=None, repr=False)
+    draw_window: tuple | None = field(default=None, repr=False)
 
 
 def greedy_token(x: np.ndarray) -> int:
@@ -117,7 +127,10 @@ def sample_row(row, dtype: str, temperature: float, top_k: int, top_p: float, u:
     temperature = float(np.float32(temperature))
     top_p = float(np.float32(top_p))
     u = float(np.float32(u))
-    if (not temperature >= 0.0) or not (0.0 < top_p <= 1.0) or top_k < 0:
+    # the C ABI's parameter contract (include/pbsample.h): a finite temperature >= 0,
+    # top_p in (0, 1], top_k >= 0 (an infinite temperature, which SamplingParams lets
+    # through, is rejected there too)
+    if (not temperature >= 0.0) or not np.isfinite(temperature) or not (0.0 < top_p <= 1.0) or top_k < 0:
         return RowResult(token=0, status=ROW_BAD_PARAM)
     if temperature == 0.0:  # SamplingParams.greedy, config.py:156-158
         return RowResult(token=greedy_token(x32))
@@ -186,6 +199,11 @@ def sample_row(row, dtype: str, temperature: float, top_k: int, top_p: float, u:
     lo = ck[j - 1] if j > 0 else 0.0
     hi = ck[j]
     res.draw_margin = float(min(abs(t - lo), abs(hi - t)) / z_p)
+    if top_p < 1.0:
+        a, b = max(0, n_keep_sorted - WINDOW), min(order.size, n_keep_sorted + WINDOW)
+        res.cut_window = (a, order[a:b].copy(), excl[a:b] / z_k)
+    a, b = max(0, j - 4), min(order.size, j + 5)
+    res.draw_window = (a, order[a:b].copy(), excl[a:b] / z_p, csum[a:b] / z_p)
 
     if want_probs:
         kept = np.zeros(V, dtype=bool)

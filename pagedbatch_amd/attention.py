@@ -17,6 +17,43 @@ from . import _lib
 from .sampling import SamplerError
 
 
+HEAD_DIM = 64  # the only head size the kernel serves (k_decode indexes [slot][kv_head][64])
+
+
+def _check_args(q, k_cache, v_cache, block_table, context_lens) -> None:
+    """Shapes, dtypes, devices and alignment of every operand, before anything reaches the
+    kernel: it indexes the caches as [n_slots][n_kv_heads][64] bf16 through 16-byte loads
+    and reads every pointer on q's device, so a smaller cache head size, a host tensor or
+    a misaligned view would be read out of bounds instead of failing here."""
+    if q.dtype != torch.float32 or q.dim() != 3 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous fp32 [rows, n_heads, head_dim] tensor")
+    rows, n_heads, head_dim = q.shape
+    if head_dim != HEAD_DIM:
+        raise ValueError(f"head_dim must be {HEAD_DIM}, got {head_dim}")
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if c.dtype != torch.bfloat16 or c.dim() != 3 or not c.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 [n_slots, n_kv_heads, head_dim] tensor")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache differ in shape")
+    if k_cache.shape[2] != head_dim:
+        raise ValueError(f"the caches' head_dim {k_cache.shape[2]} differs from q's {head_dim}")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
+        raise ValueError("block_table must be a contiguous int32 [rows, max_blocks] tensor")
+    if context_lens.dtype != torch.int32 or context_lens.dim() != 1 or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be a contiguous int32 [rows] tensor")
+    if block_table.shape[0] != rows or context_lens.shape[0] != rows:
+        raise ValueError("block_table and context_lens need one row per query row")
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
+                    ("context_lens", context_lens)):
+        if t.device != q.device:
+            raise ValueError(f"{name} is on {t.device}, q on {q.device}: every operand must be on q's device")
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.data_ptr() % 16:
+            raise ValueError(f"{name} must start on a 16-byte boundary (the kernel reads it in 16-byte loads)")
+    if not q.is_cuda:
+        raise ValueError("the operands must live on a ROCm device; decode_attention has no CPU path")
+
+
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
                      context_lens: torch.Tensor, block_size: int, max_context: int,
                      scale: float | None = None) -> torch.Tensor:
@@ -24,21 +61,9 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     block_table: int32 [rows, max_blocks]; context_lens: int32 [rows], each in
     [1, max_context]. Returns fp32 [rows, n_heads, 64]. Asynchronous on the current
     stream; a sequence whose block table points outside the pools gets NaN."""
-    if q.dtype != torch.float32 or q.dim() != 3 or not q.is_contiguous() or not q.is_cuda:
-        raise ValueError("q must be a contiguous fp32 [rows, n_heads, head_dim] device tensor")
-    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
-        if c.dtype != torch.bfloat16 or c.dim() != 3 or not c.is_contiguous():
-            raise ValueError(f"{name} must be a contiguous bf16 [n_slots, n_kv_heads, head_dim] tensor")
-    if k_cache.shape != v_cache.shape:
-        raise ValueError("k_cache and v_cache differ in shape")
-    if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
-        raise ValueError("block_table must be a contiguous int32 [rows, max_blocks] tensor")
-    if context_lens.dtype != torch.int32 or context_lens.dim() != 1 or not context_lens.is_contiguous():
-        raise ValueError("context_lens must be a contiguous int32 [rows] tensor")
+    _check_args(q, k_cache, v_cache, block_table, context_lens)
     rows, n_heads, head_dim = q.shape
     n_slots, n_kv_heads, _ = k_cache.shape
-    if block_table.shape[0] != rows or context_lens.shape[0] != rows:
-        raise ValueError("block_table and context_lens need one row per query row")
     out = torch.empty_like(q)
     lib = _lib.load()
     rc = lib.pba_decode_attention(

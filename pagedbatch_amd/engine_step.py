@@ -19,14 +19,17 @@ from __future__ import annotations
 
 import math
 import time
-from dataclasses import dataclass
+from dataclasses import dataclass, field
+
+import numpy as np
 
 import torch
 import torch.nn.functional as F
 
 from .attention import decode_attention
 from .config import SamplingParams
-from .sampling import sample
+from .finish import FinishRule
+from .sampling import _uniforms, sample_and_finish
 
 
 @dataclass
@@ -169,28 +172,45 @@ class PagedKV:
 
 
 @dataclass
+class StepCapture:
+    """What one step handed the sampler and got back: the logits (a device copy), the
+    per-row parameters, the uniforms the rows drew and the tokens."""
+
+    step: int
+    logits: torch.Tensor
+    temperature: list
+    top_k: list
+    top_p: list
+    uniform: np.ndarray
+    tokens: list
+
+
+@dataclass
 class StepTimes:
     """Per-step wall times (s): the forward (logits ready on the device) and the sampling
-    call (params, uniforms, launch, kernel, token copy back). Step 0 is the prefill."""
+    call (params, uniforms, launch, kernel, stop check, tokens and reasons copied back).
+    Step 0 is the prefill. ``reasons`` holds each step's finish reasons (engine.py:173-182)
+    from the batched call; ``captures`` the steps asked for with ``capture_steps``."""
 
-    forward_s: list = None
-    sample_s: list = None
+    forward_s: list = field(default_factory=list)
+    sample_s: list = field(default_factory=list)
     tokens_per_step: int = 0
-
-    def __post_init__(self):
-        self.forward_s = []
-        self.sample_s = []
+    reasons: list = field(default_factory=list)
+    captures: list = field(default_factory=list)
 
 
 def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len: int = 128, block_size: int = 16,
         device: str | torch.device = "cuda", seed: int = 0, per_row: bool = False,
-        fused_decode: bool = False) -> tuple[StepTimes, list[list[int]]]:
+        fused_decode: bool = False, capture_steps=()) -> tuple[StepTimes, list[list[int]]]:
     """Prefill every prompt, then decode in lockstep until each request has ``output_len``
     tokens. Half the requests are greedy, half top-k=50 / top-p=0.9 at temperature 1.0; the
-    unseeded ones share one engine generator (engine.py:58). ``per_row`` samples with one
-    ``sample_token`` call per sequence (the reference loop, unhoisted) instead of one batched
-    ``sample``; ``fused_decode`` runs the decode steps' attention through the paged-attention
-    kernel. Returns the time split and the generated tokens."""
+    unseeded ones share one engine generator (engine.py:58). The batched path samples with
+    one ``sample_and_finish`` call per step (the hoist of engine.py:133-139 with the stop
+    check of engine.py:173-182 in the same launch sequence and copy back; the model has no
+    EOS here, so every request runs to its length limit); ``per_row`` samples with one
+    ``sample_token`` call per sequence (the reference loop, unhoisted). ``fused_decode``
+    runs the decode steps' attention through the paged-attention kernel. Returns the time
+    split and the generated tokens."""
     device = torch.device(device)
     model = Model(shape, device, seed=seed)
     cache = PagedKV(shape, num_seqs, prompt_len + output_len, block_size, device, torch.bfloat16)
@@ -198,13 +218,15 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
     prompts = torch.randint(3, shape.vocab_size, (num_seqs, prompt_len), generator=g)
     params = [SamplingParams(temperature=0.0) if i % 2 == 0 else SamplingParams(temperature=1.0, top_k=50, top_p=0.9)
               for i in range(num_seqs)]
+    temps = np.array([p.temperature for p in params])
     engine_gen = torch.Generator().manual_seed(seed + 2)
     gens = [engine_gen] * num_seqs
     seq = torch.arange(num_seqs, device=device)
     out: list[list[int]] = [[] for _ in range(num_seqs)]
     times = StepTimes(tokens_per_step=num_seqs)
+    capture_steps = set(capture_steps)
 
-    def step(tokens: torch.Tensor, start: int, q_len: int) -> list[int]:
+    def step(idx: int, tokens: torch.Tensor, start: int, q_len: int) -> list[int]:
         pos = torch.arange(start, start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
         slots = cache.slots(seq.view(-1, 1), pos).reshape(-1)
         ctx = torch.arange(start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
@@ -214,22 +236,38 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
         logits = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache, fused_decode)
         torch.cuda.synchronize(device)
         t1 = time.perf_counter()
+        cap = None
+        if idx in capture_steps:
+            # the uniforms this step's rows will draw: from a copy of the engine generator
+            snap = torch.Generator().manual_seed(0)
+            snap.set_state(engine_gen.get_state())
+            cap = StepCapture(idx, logits.clone(), [p.temperature for p in params], [p.top_k for p in params],
+                              [p.top_p for p in params], _uniforms(temps, [snap] * num_seqs), [])
+            torch.cuda.synchronize(device)
+            t1 = time.perf_counter()
         if per_row:
             from .sampling import sample_token
             toks = [sample_token(logits[i], params[i], gens[i]) for i in range(num_seqs)]
         else:
-            toks = sample(logits, params, gens)
+            n_out = len(out[0]) + 1  # outputs after this token (lockstep)
+            rules = [FinishRule(ignore_eos=False, stop_token_ids=(), num_output=n_out, max_tokens=output_len,
+                                num_tokens=prompt_len + n_out)] * num_seqs
+            toks, reasons = sample_and_finish(logits, params, gens, rules, None, prompt_len + output_len)
+            times.reasons.append(reasons)
         t2 = time.perf_counter()
         times.forward_s.append(t1 - t0)
         times.sample_s.append(t2 - t1)
+        if cap is not None:
+            cap.tokens = list(toks)
+            times.captures.append(cap)
         return toks
 
-    toks = step(prompts.to(device), 0, prompt_len)
+    toks = step(0, prompts.to(device), 0, prompt_len)
     for i, t in enumerate(toks):
         out[i].append(t)
     for n in range(1, output_len):
         cur = torch.tensor([o[-1] for o in out], device=device).view(-1, 1)
-        toks = step(cur, prompt_len + n - 1, 1)
+        toks = step(n, cur, prompt_len + n - 1, 1)
         for i, t in enumerate(toks):
             out[i].append(t)
     return times, out

@@ -3,7 +3,9 @@
 ``sample_token`` keeps the signature of pagedbatch/sampling.py:10 so the reference engine
 can import it unchanged. ``sample`` is the batched form the engine's per-row loop
 (pagedbatch/engine.py:133-139) can be hoisted into: one kernel launch and one
-device-to-host copy per step instead of one sync per row.
+device-to-host copy per step instead of one sync per row. ``sample_and_finish`` also runs
+the step's stop check (engine.py:173-182) on the device and brings the finish reasons back
+in the same copy as the tokens.
 
 The draw consumes one uniform per stochastic row, taken from that row's generator with
 ``torch.rand`` in row order (greedy rows consume nothing, as in the reference), and picks
@@ -16,8 +18,10 @@ consumes differs (one number per row instead of ``vocab``).
 from __future__ import annotations
 
 import threading
+import time
 from collections.abc import Sequence
 from dataclasses import dataclass
+from operator import attrgetter
 
 import numpy as np
 import torch
@@ -28,6 +32,8 @@ _TORCH_DTYPE = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, to
 
 # torch.multinomial's message for an invalid distribution (what the reference raises)
 _BAD_PROBS = "probability tensor contains either `inf`, `nan` or element < 0"
+
+_TEMPERATURE, _TOP_K, _TOP_P = attrgetter("temperature"), attrgetter("top_k"), attrgetter("top_p")
 
 
 class SamplerError(RuntimeError):
@@ -43,25 +49,39 @@ class DebugOutput:
     kept: torch.Tensor | None  # uint8 [rows, vocab] on the device
 
 
+# staging layout, in int32 words of one pinned host block and its device copy:
+#   inputs   temperature f32 | top_k i32 | top_p f32 | uniform f32 | row_map i32   (cap each)
+#   finish   stop_offsets [cap + 1] | num_output | max_tokens | num_tokens  (cap each)
+#            | ignore_eos u8 [cap] (cap / 4 words) | stop_ids [stop_cap]
+#   outputs  token i32 | status i32 | reason i32   (cap each, a block of their own)
+_IN_T, _IN_K, _IN_P, _IN_U, _IN_MAP = range(5)
+
+
 class _Buffers:
     """Per-device staging: pinned host + device copies of the packed per-row arrays."""
 
     def __init__(self, device: torch.device):
         self.device = device
         self.cap = 0
+        self.stop_cap = 0
         self.lock = threading.Lock()
 
-    def ensure(self, n: int) -> None:
-        if n <= self.cap:
+    def ensure(self, n: int, nstop: int = 0) -> None:
+        if n <= self.cap and nstop <= self.stop_cap:
             return
-        cap = max(64, 1 << (n - 1).bit_length())
-        # [temperature f32 | top_k i32 | top_p f32 | uniform f32 | row_map i32] x cap
-        self.h_in = torch.empty(5 * cap, dtype=torch.int32, pin_memory=True)
-        self.d_in = torch.empty(5 * cap, dtype=torch.int32, device=self.device)
-        # [token i32 | status i32] x cap
-        self.h_out = torch.empty(2 * cap, dtype=torch.int32, pin_memory=True)
-        self.d_out = torch.empty(2 * cap, dtype=torch.int32, device=self.device)
+        cap = max(64, 1 << (max(n, self.cap) - 1).bit_length())
+        stop_cap = max(self.stop_cap, 64, 1 << max(0, nstop - 1).bit_length())
+        self.fin = 5 * cap  # start of the finish block
+        self.stop_ids = self.fin + (cap + 1) + 3 * cap + cap // 4
+        words = self.stop_ids + stop_cap
+        self.h_in = torch.empty(words, dtype=torch.int32, pin_memory=True)
+        self.d_in = torch.empty(words, dtype=torch.int32, device=self.device)
+        self.h_in_np = self.h_in.numpy()
+        self.h_out = torch.empty(3 * cap, dtype=torch.int32, pin_memory=True)
+        self.d_out = torch.empty(3 * cap, dtype=torch.int32, device=self.device)
+        self.h_out_np = self.h_out.numpy()
         self.cap = cap
+        self.stop_cap = stop_cap
 
 
 _buffers: dict[int, _Buffers] = {}
@@ -91,24 +111,87 @@ def _check_logits(logits: torch.Tensor) -> torch.Tensor:
     return logits
 
 
-def _top_k_code(k: int, vocab: int) -> int:
-    # pagedbatch applies top-k only when 0 < k < vocab (sampling.py:15)
-    return int(k) if 0 < int(k) < vocab else 0
+def _top_k_codes(top_k, vocab: int) -> np.ndarray:
+    """The kernel's top_k argument: pagedbatch applies top-k only when 0 < k < vocab
+    (sampling.py:15), so k >= vocab becomes 0 (off); a negative k stays negative (-1) so
+    that the kernel reports the row as a bad parameter instead of switching top-k off."""
+    k = np.asarray(top_k, dtype=np.int64)
+    return np.where(k < 0, -1, np.where(k < vocab, k, 0)).astype(np.int32)
 
 
-def _launch(logits, h: np.ndarray, n: int, row_map_given: bool, debug: bool, bufs: _Buffers):
-    """Copy packed params (host int32 view ``h``) and call the C ABI. Returns device outputs."""
-    lib = _lib.load()
-    hin = bufs.h_in.numpy()
+def _pack(n, temperature, top_k, top_p, uniform, row_map, vocab) -> np.ndarray:
+    """The five per-row parameter arrays as one int32 [5, n] block (the staging layout)."""
+    h = np.zeros((5, n), dtype=np.int32)
+    h[_IN_T] = np.asarray(temperature, dtype=np.float32).view(np.int32)
+    h[_IN_K] = _top_k_codes(top_k, vocab)
+    h[_IN_P] = np.asarray(top_p, dtype=np.float32).view(np.int32)
+    h[_IN_U] = np.asarray(uniform, dtype=np.float32).view(np.int32)
+    if row_map is not None:
+        h[_IN_MAP] = np.asarray(row_map, dtype=np.int32)
+    return h
+
+
+def _stage_params(bufs: _Buffers, h: np.ndarray, n: int) -> None:
     cap = bufs.cap
     for i in range(5):
-        hin[i * cap : i * cap + n] = h[i]
-    bufs.d_in.copy_(bufs.h_in, non_blocking=True)
+        bufs.h_in_np[i * cap : i * cap + n] = h[i]
+
+
+def _stage_finish(bufs: _Buffers, rules, n: int) -> int:
+    """The stop rules of n rows into the finish block; returns the number of stop ids."""
+    return _write_finish(bufs.h_in_np, bufs.fin, bufs.cap, bufs.stop_ids, rules, n)
+
+
+def _write_finish(hin: np.ndarray, base: int, cap: int, stop_base: int, rules, n: int) -> int:
+    """Finish block layout (int32 words from ``base``): stop_offsets [cap + 1], num_output,
+    max_tokens, num_tokens [cap each], ignore_eos bytes [cap]; stop ids from ``stop_base``."""
+    lens = np.fromiter((len(r.stop_token_ids) for r in rules), np.int64, n)
+    offs = hin[base : base + n + 1]
+    offs[0] = 0
+    offs[1:] = np.cumsum(lens)
+    o = base + cap + 1
+    hin[o : o + n] = np.fromiter((r.num_output for r in rules), np.int32, n)
+    hin[o + cap : o + cap + n] = np.fromiter((r.max_tokens for r in rules), np.int32, n)
+    hin[o + 2 * cap : o + 2 * cap + n] = np.fromiter((r.num_tokens for r in rules), np.int32, n)
+    ign = hin[o + 3 * cap : o + 3 * cap + cap // 4].view(np.uint8)
+    ign[:n] = np.fromiter((1 if r.ignore_eos else 0 for r in rules), np.uint8, n)
+    nstop = int(offs[n])
+    if nstop:
+        hin[stop_base : stop_base + nstop] = [t for r in rules for t in r.stop_token_ids]
+    return nstop
+
+
+def _raise_for_status(status: np.ndarray, temperature: np.ndarray | None = None) -> None:
+    bad = np.flatnonzero(status != _lib.ROW_OK)
+    if bad.size == 0:
+        return
+    b = int(bad[0])
+    code = int(status[b])
+    if code == _lib.ROW_BAD_PARAM:
+        if temperature is not None and np.isnan(temperature[b]):
+            # a NaN temperature passes SamplingParams' check (config.py:146) and reaches
+            # multinomial as NaN probabilities in the reference (sampling.py:27)
+            raise RuntimeError(_BAD_PROBS)
+        raise ValueError(f"invalid sampling parameters or row index for row {b} "
+                         "(temperature must be finite, top_p in (0, 1], top_k >= 0)")
+    raise RuntimeError(_BAD_PROBS)
+
+
+def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, finish=None, timing=None):
+    """Copy the staged params to the device and call the C ABI; with ``finish`` (eos id,
+    max_model_len, number of stop ids) also the stop check, on the sampler's device tokens.
+    Returns host tokens, statuses and reasons (None without ``finish``) plus the device
+    diagnostics of a debug call."""
+    lib = _lib.load()
+    cap = bufs.cap
+    stream = torch.cuda.current_stream(logits.device)
+    sp = stream.cuda_stream
+    words = bufs.fin if finish is None else bufs.stop_ids + finish[2]
+    bufs.d_in[:words].copy_(bufs.h_in[:words], non_blocking=True)
     base = bufs.d_in.data_ptr()
     ptr = [base + 4 * i * cap for i in range(5)]
     out_tok = bufs.d_out.data_ptr()
     out_st = out_tok + 4 * cap
-    stream = torch.cuda.current_stream(logits.device).cuda_stream
     args = [
         logits.data_ptr(),
         _TORCH_DTYPE[logits.dtype],
@@ -116,11 +199,11 @@ def _launch(logits, h: np.ndarray, n: int, row_map_given: bool, debug: bool, buf
         n,
         logits.shape[1],
         logits.stride(0),
-        ptr[4] if row_map_given else None,
-        ptr[0],
-        ptr[1],
-        ptr[2],
-        ptr[3],
+        ptr[_IN_MAP] if row_map_given else None,
+        ptr[_IN_T],
+        ptr[_IN_K],
+        ptr[_IN_P],
+        ptr[_IN_U],
         out_tok,
         out_st,
     ]
@@ -130,9 +213,9 @@ def _launch(logits, h: np.ndarray, n: int, row_map_given: bool, debug: bool, buf
         probs = torch.empty((n, V), dtype=torch.float32, device=logits.device)
         kept = torch.empty((n, V), dtype=torch.uint8, device=logits.device)
         info = torch.empty(n * _lib.ROW_INFO_DTYPE.itemsize, dtype=torch.uint8, device=logits.device)
-        rc = lib.pbs_sample_debug(*args, probs.data_ptr(), kept.data_ptr(), info.data_ptr(), None, 0, stream)
+        rc = lib.pbs_sample_debug(*args, probs.data_ptr(), kept.data_ptr(), info.data_ptr(), None, 0, sp)
     else:
-        rc = lib.pbs_sample(*args, None, 0, stream)
+        rc = lib.pbs_sample(*args, None, 0, sp)
     if rc != _lib.OK:
         msg = _lib.last_error(lib)
         if rc == _lib.ERR_INVALID_ARGUMENT:
@@ -140,33 +223,55 @@ def _launch(logits, h: np.ndarray, n: int, row_map_given: bool, debug: bool, buf
         if rc == _lib.ERR_UNSUPPORTED_DTYPE:
             raise TypeError(msg)
         raise SamplerError(f"pbs_sample failed ({rc}): {msg}")
-    bufs.h_out.copy_(bufs.d_out, non_blocking=True)
-    torch.cuda.current_stream(logits.device).synchronize()
-    hout = bufs.h_out.numpy()
+    nout = 2
+    if finish is not None:
+        eos, max_model_len, nstop = finish
+        f = base + 4 * bufs.fin
+        o = f + 4 * (cap + 1)
+        rc = lib.pbs_finish_reasons(out_tok, n, -1 if eos is None else int(eos), o + 4 * 3 * cap, f,
+                                    base + 4 * bufs.stop_ids if nstop else None, o, o + 4 * cap, o + 8 * cap,
+                                    int(max_model_len), out_tok + 8 * cap, sp)
+        if rc != _lib.OK:
+            raise SamplerError(f"pbs_finish_reasons failed ({rc}): {_lib.last_error(lib)}")
+        nout = 3
+    bufs.h_out[: nout * cap].copy_(bufs.d_out[: nout * cap], non_blocking=True)
+    stream.synchronize()
+    if timing is not None:
+        timing["launch_sync"] = time.perf_counter()
+    hout = bufs.h_out_np
     tokens = hout[:n].copy()
     status = hout[cap : cap + n].copy()
-    return tokens, status, probs, kept, info
+    reasons = hout[2 * cap : 2 * cap + n].copy() if finish is not None else None
+    return tokens, status, reasons, probs, kept, info
 
 
-def _pack(n, temperature, top_k, top_p, uniform, row_map, vocab) -> np.ndarray:
-    h = np.zeros((5, n), dtype=np.int32)
-    h[0] = np.asarray(temperature, dtype=np.float32).view(np.int32)
-    h[1] = np.asarray([_top_k_code(k, vocab) for k in top_k], dtype=np.int32)
-    h[2] = np.asarray(top_p, dtype=np.float32).view(np.int32)
-    h[3] = np.asarray(uniform, dtype=np.float32).view(np.int32)
-    if row_map is not None:
-        h[4] = np.asarray(row_map, dtype=np.int32)
-    return h
-
-
-def _raise_for_status(status: np.ndarray) -> None:
-    bad = np.flatnonzero(status != _lib.ROW_OK)
-    if bad.size == 0:
-        return
-    code = int(status[bad[0]])
-    if code == _lib.ROW_BAD_PARAM:
-        raise ValueError(f"invalid sampling parameters or row index for row {int(bad[0])}")
-    raise RuntimeError(_BAD_PROBS)
+def _uniforms(temperature: np.ndarray, generators: Sequence[torch.Generator]) -> np.ndarray:
+    """One uniform per stochastic row (temperature != 0), in row order, float32."""
+    n = temperature.shape[0]
+    out = np.zeros(n, dtype=np.float32)
+    idx = np.flatnonzero(temperature != 0)
+    if idx.size == 0:
+        return out
+    g0 = generators[int(idx[0])]
+    if all(generators[i] is g0 for i in idx.tolist()):
+        # every stochastic row shares one generator (the engine's, engine.py:58): one call
+        out[idx] = torch.rand(idx.size, generator=g0, device=g0.device).numpy()
+        return out
+    # runs of consecutive stochastic rows (greedy rows between them draw nothing) sharing a
+    # generator: one torch.rand per run
+    rows = idx.tolist()
+    i = 0
+    while i < len(rows):
+        g = generators[rows[i]]
+        j = i + 1
+        while j < len(rows) and generators[rows[j]] is g:
+            j += 1
+        if j - i == 1:
+            out[rows[i]] = float(torch.rand((), generator=g, device=g.device))
+        else:
+            out[rows[i:j]] = torch.rand(j - i, generator=g, device=g.device).numpy()
+        i = j
+    return out
 
 
 def draw_uniforms(params: Sequence, generators: Sequence[torch.Generator]) -> list[float]:
@@ -177,25 +282,56 @@ def draw_uniforms(params: Sequence, generators: Sequence[torch.Generator]) -> li
     fills it with the same numbers, in the same order, as n scalar draws, and leaves the
     generator in the same state.
     """
-    out = [0.0] * len(params)
-    i, n = 0, len(params)
-    while i < n:
-        if params[i].temperature == 0:
-            i += 1
-            continue
-        g = generators[i]
-        j = i + 1
-        idx = [i]
-        # extend the run over greedy rows (which draw nothing) while the generator repeats
-        while j < n and (params[j].temperature == 0 or generators[j] is g):
-            if params[j].temperature != 0:
-                idx.append(j)
-            j += 1
-        vals = torch.rand(len(idx), generator=g, device=g.device).tolist()
-        for k, v in zip(idx, vals):
-            out[k] = float(v)
-        i = j
-    return out
+    t = np.fromiter(map(_TEMPERATURE, params), np.float64, len(params))
+    return [float(v) for v in _uniforms(t, generators)]
+
+
+def _param_arrays(params: Sequence, n: int):
+    t = np.fromiter(map(_TEMPERATURE, params), np.float64, n)
+    k = np.fromiter(map(_TOP_K, params), np.int64, n)
+    p = np.fromiter(map(_TOP_P, params), np.float64, n)
+    # SamplingParams' own checks (config.py:146-154), for objects built without them
+    if (t < 0).any() or not ((p > 0) & (p <= 1)).all() or (k < 0).any():
+        raise ValueError("invalid SamplingParams")
+    return t, k, p
+
+
+def _sample(logits, params, generators, rows, finish_rules=None, eos_token_id=None, max_model_len=0,
+            timing=None):
+    logits = _check_logits(logits)
+    n = len(rows) if rows is not None else logits.shape[0]
+    if len(params) != n or len(generators) != n:
+        raise ValueError(f"need {n} params and generators, got {len(params)} and {len(generators)}")
+    if finish_rules is not None and len(finish_rules) != n:
+        raise ValueError(f"need {n} finish rules, got {len(finish_rules)}")
+    if n == 0:
+        return [], ([] if finish_rules is not None else None)
+    if timing is not None:
+        timing["start"] = time.perf_counter()
+    t, k, p = _param_arrays(params, n)
+    u = _uniforms(t, generators)
+    if timing is not None:
+        timing["uniforms"] = time.perf_counter()
+    h = _pack(n, t, k, p, u, rows, logits.shape[1])
+    bufs = _buffers_for(logits.device)
+    with bufs.lock:
+        nstop = sum(len(r.stop_token_ids) for r in finish_rules) if finish_rules is not None else 0
+        bufs.ensure(n, nstop)
+        _stage_params(bufs, h, n)
+        fin = None
+        if finish_rules is not None:
+            fin = (eos_token_id, max_model_len, _stage_finish(bufs, finish_rules, n))
+        if timing is not None:
+            timing["pack"] = time.perf_counter()
+        tokens, status, reasons, _, _, _ = _launch(logits, n, rows is not None, False, bufs, finish=fin,
+                                                   timing=timing)
+    _raise_for_status(status, t)
+    toks = tokens.tolist()
+    if finish_rules is None:
+        return toks, None
+    from .finish import REASONS
+
+    return toks, [REASONS[c] for c in reasons.tolist()]
 
 
 def sample(logits: torch.Tensor, params: Sequence, generators: Sequence[torch.Generator],
@@ -207,25 +343,18 @@ def sample(logits: torch.Tensor, params: Sequence, generators: Sequence[torch.Ge
     uniforms are drawn in, matching the reference's per-row loop over one shared engine
     generator.
     """
-    logits = _check_logits(logits)
-    n = len(rows) if rows is not None else logits.shape[0]
-    if len(params) != n or len(generators) != n:
-        raise ValueError(f"need {n} params and generators, got {len(params)} and {len(generators)}")
-    if n == 0:
-        return []
-    for sp in params:
-        if sp.temperature < 0 or not 0 < sp.top_p <= 1 or sp.top_k < 0:
-            raise ValueError("invalid SamplingParams")
-    uniforms = draw_uniforms(params, generators)
-    V = logits.shape[1]
-    h = _pack(n, [sp.temperature for sp in params], [sp.top_k for sp in params], [sp.top_p for sp in params],
-              uniforms, rows, V)
-    bufs = _buffers_for(logits.device)
-    with bufs.lock:
-        bufs.ensure(n)
-        tokens, status, _, _, _ = _launch(logits, h, n, rows is not None, False, bufs)
-    _raise_for_status(status)
-    return [int(t) for t in tokens]
+    return _sample(logits, params, generators, rows)[0]
+
+
+def sample_and_finish(logits: torch.Tensor, params: Sequence, generators: Sequence[torch.Generator],
+                      rules: Sequence, eos_token_id: int | None, max_model_len: int,
+                      rows: Sequence[int] | None = None) -> tuple[list[int], list[str | None]]:
+    """``sample`` plus the stop check of each sampled sequence after its new token
+    (pagedbatch/engine.py:173-182, with ``rules[i]`` a ``finish.FinishRule`` that counts
+    the new token): the check runs on the device right after the sampling kernel and the
+    reasons ("stop", "length" or None) come back in the tokens' copy."""
+    return _sample(logits, params, generators, rows, finish_rules=rules, eos_token_id=eos_token_id,
+                   max_model_len=max_model_len)
 
 
 def sample_token(logits: torch.Tensor, params, generator: torch.Generator) -> int:
@@ -250,9 +379,10 @@ def sample_arrays(logits: torch.Tensor, temperature, top_k, top_p, uniform, row_
     bufs = _buffers_for(logits.device)
     with bufs.lock:
         bufs.ensure(n)
-        tokens, status, probs, kept, info = _launch(logits, h, n, row_map is not None, debug, bufs)
+        _stage_params(bufs, h, n)
+        tokens, status, _, probs, kept, info = _launch(logits, n, row_map is not None, debug, bufs)
     if check:
-        _raise_for_status(status)
+        _raise_for_status(status, np.asarray(temperature, dtype=np.float64))
     if not debug:
         return tokens, status
     info_np = np.frombuffer(info.cpu().numpy().tobytes(), dtype=_lib.ROW_INFO_DTYPE).copy()

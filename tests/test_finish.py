@@ -129,3 +129,33 @@ def test_finish_after_sampling_on_device():
     rules = [FinishRule(False, (), 1, 10, 5), FinishRule(False, (17,), 1, 10, 5), FinishRule(False, (17,), 10, 10, 14)]
     got = finish_reasons(torch.from_numpy(np.asarray(tok, np.int32)).to(dev), rules, 2, 2048)
     assert got == ["stop", "stop", "length"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [3, 300])
+def test_sample_and_finish_matches_the_oracle(n):
+    """sample_and_finish: the sampler's tokens and, in the same copy back, the stop check
+    of every row (engine.py:173-182) against the oracle on the tokens it produced; the
+    tokens equal a plain sample() on the same inputs."""
+    from pagedbatch_amd import SamplingParams, sample
+    from pagedbatch_amd.sampling import sample_and_finish
+
+    print(f"[case] sample_and_finish n={n}", flush=True)
+    dev = torch.device("cuda", 0)
+    rules, want_tok = _random_rules(n, 5 + n, 2)
+    # greedy rows whose argmax is the planted token, so that EOS, stop ids and plain
+    # tokens all occur; every fifth row stochastic
+    x = torch.zeros(n, 64)
+    x[torch.arange(n), torch.tensor(want_tok)] = 8.0
+    params = [SamplingParams(temperature=0.0) if i % 5 else SamplingParams(temperature=1.0, top_k=3)
+              for i in range(n)]
+    g1, g2 = torch.Generator().manual_seed(4), torch.Generator().manual_seed(4)
+    logits = x.to(dev)
+    toks, reasons = sample_and_finish(logits, params, [g1] * n, rules, 2, 150)
+    assert toks == sample(logits, params, [g2] * n)
+    assert all(t == w for i, (t, w) in enumerate(zip(toks, want_tok)) if i % 5)
+    want = [finish_reason(t, 2, r.ignore_eos, r.stop_token_ids, r.num_output, r.max_tokens, r.num_tokens, 150)
+            for t, r in zip(toks, rules)]
+    assert reasons == want
+    if n >= 300:
+        assert {None, "stop", "length"} <= set(reasons)

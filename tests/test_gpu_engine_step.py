@@ -1,15 +1,56 @@
-"""The engine-step harness (pagedbatch_amd.engine_step): one batched sampling call per step
-gives the same tokens as one call per row (the reference's loop, engine.py:133-139), and
-greedy rows follow the logits' argmax."""
+"""The engine-step harness (pagedbatch_amd.engine_step) on the GPU.
+
+* The configuration the engine benchmark runs (a smollm2-135m-shaped random bf16 model, 64
+  requests of 128 prompt tokens, half greedy and half top-k=50 / top-p=0.9, block size 16):
+  every captured step's tokens against the oracle on that step's own logits and
+  uniforms (pagedbatch/engine.py:130-139 samples these rows one by one), greedy rows bit
+  for bit, and the finish reasons the batched call brings back (engine.py:173-182).
+* One batched sampling call per step gives the same tokens as one call per row (the
+  reference's loop, engine.py:133-139); greedy rows follow the logits' argmax.
+"""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
+from oracle import oracle
+from oracle.compare import compare_rows
 from pagedbatch_amd import engine_step as es
+from pagedbatch_amd.sampling import sample_arrays
 
 pytestmark = pytest.mark.gpu
+
+
+def test_smollm2_64_requests_match_the_oracle(dev):
+    """Prefill plus three decode steps at the benchmark's shape, decode attention through
+    the paged-attention kernel; each step's sampling checked against the oracle."""
+    steps = 4
+    print("[case] engine step smollm2-135m shape, 64 requests, 4 steps", flush=True)
+    times, out = es.run(es.ModelShape(), num_seqs=64, prompt_len=128, output_len=steps, block_size=16, device=dev,
+                        fused_decode=True, capture_steps=range(steps))
+    assert len(times.captures) == steps and all(len(o) == steps for o in out)
+    for cap in times.captures:
+        greedy = [t == 0 for t in cap.temperature]
+        raw = cap.logits.cpu().view(torch.int16).numpy().view(np.uint16)
+        refs = oracle.sample_batch(raw, "bfloat16", cap.temperature, cap.top_k, cap.top_p, cap.uniform,
+                                   want_probs=True)
+        dbg = sample_arrays(cap.logits, cap.temperature, cap.top_k, cap.top_p, cap.uniform, debug=True)
+        # the engine's own call and the diagnostic call agree on the same inputs
+        assert list(dbg.tokens) == cap.tokens
+        assert (dbg.status == 0).all()
+        rep = compare_rows(dbg.tokens, dbg.status, refs, greedy, probs=dbg.probs.cpu().numpy(),
+                           kept=dbg.kept.cpu().numpy(), info=dbg.info, top_p=cap.top_p, uniform=cap.uniform)
+        exact = rep.checked_tokens - sum(greedy)
+        print(f"[case] step {cap.step}: {rep.summary()} exactly checked stochastic rows {exact}/32", flush=True)
+        assert rep.ok(), rep.summary()
+        assert [int(t) for t, g in zip(dbg.tokens, greedy) if g] == [r.token for r, g in zip(refs, greedy) if g]
+        assert exact >= 16
+    # every request reaches its 4 outputs together: no reason before the last step,
+    # "length" for all at it (the random model has no EOS here)
+    assert all(r is None for rs in times.reasons[:-1] for r in rs)
+    assert times.reasons[-1] == ["length"] * 64
 
 
 def test_batched_equals_per_row_tiny_model(dev):

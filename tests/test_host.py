@@ -85,6 +85,55 @@ def test_draw_uniforms_mixed_generators_match_scalar_draws():
         assert float(torch.rand((), generator=a)) == float(torch.rand((), generator=b))
 
 
+def test_top_k_codes():
+    """top_k as the kernel gets it: 0 < k < V kept, k >= V off (sampling.py:15), a negative
+    k passed on as -1 so that the kernel flags the row instead of silently sampling it."""
+    assert list(smp._top_k_codes([0, 1, 999, 1000, 10**12, -1, -7], 1000)) == [0, 1, 999, 0, 0, -1, -1]
+    h = smp._pack(2, [1.0, 1.0], [-2, 5], [1.0, 1.0], [0.5, 0.5], None, vocab=10)
+    assert list(h[1]) == [-1, 5]
+
+
+@pytest.mark.parametrize("n", [16, 17, 64, 255, 1000, 20000])
+def test_batched_rand_equals_scalar_draws(n):
+    """torch.rand(n) gives the numbers of n scalar torch.rand draws, in order, and leaves
+    the generator where they leave it: what lets a run of rows that share a generator (the
+    engine's, engine.py:58) take its uniforms from one call."""
+    a, b = torch.Generator().manual_seed(n), torch.Generator().manual_seed(n)
+    batch = torch.rand(n, generator=a)
+    scalars = torch.tensor([float(torch.rand((), generator=b)) for _ in range(n)])
+    assert torch.equal(batch, scalars)
+    assert torch.equal(a.get_state(), b.get_state())
+
+
+def test_shared_generator_uniforms_match_scalar_draws():
+    """256 rows, every stochastic one on the shared generator (the fast path: one call)."""
+    temps = np.array([0.0 if i % 3 == 0 else 1.0 for i in range(256)])
+    g, r = torch.Generator().manual_seed(9), torch.Generator().manual_seed(9)
+    u = smp._uniforms(temps, [g] * 256)
+    want = [0.0 if t == 0 else float(torch.rand((), generator=r)) for t in temps]
+    assert u.dtype == np.float32 and list(u.astype(np.float64)) == want
+    assert torch.equal(g.get_state(), r.get_state())
+
+
+def test_finish_staging_layout():
+    """The finish block matches what _launch hands pbs_finish_reasons (engine.py:173-182
+    inputs): stop offsets, num_output, max_tokens, num_tokens, ignore_eos bytes, stop ids."""
+    from pagedbatch_amd.finish import FinishRule
+
+    rules = [FinishRule(False, (), 3, 10, 20), FinishRule(True, (5, 9), 10, 10, 30), FinishRule(False, (7,), 1, 4, 5)]
+    cap, base = 64, 7
+    stop_base = base + (cap + 1) + 3 * cap + cap // 4
+    hin = np.zeros(stop_base + 64, dtype=np.int32)
+    assert smp._write_finish(hin, base, cap, stop_base, rules, 3) == 3
+    assert list(hin[base:base + 4]) == [0, 0, 2, 3]
+    o = base + cap + 1
+    assert list(hin[o:o + 3]) == [3, 10, 1]
+    assert list(hin[o + cap:o + cap + 3]) == [10, 10, 4]
+    assert list(hin[o + 2 * cap:o + 2 * cap + 3]) == [20, 30, 5]
+    assert list(hin[o + 3 * cap:o + 3 * cap + 1].view(np.uint8)[:3]) == [0, 1, 0]
+    assert list(hin[stop_base:stop_base + 3]) == [5, 9, 7]
+
+
 def test_no_cpu_path():
     x = torch.randn(2, 100)
     with pytest.raises(ValueError, match="no CPU path"):
@@ -233,3 +282,35 @@ def test_attention_abi_rejects_bad_arguments(kw, msg):
 
 def test_attention_abi_zero_rows_is_a_no_op():
     assert _attn(_lib.load(), rows=0) == _lib.OK
+
+
+# ---------------------------------------------------------------- decode_attention's checks
+def _attn_tensors(**kw):
+    t = dict(q=torch.zeros(2, 9, 64), k=torch.zeros(64, 3, 64, dtype=torch.bfloat16),
+             v=torch.zeros(64, 3, 64, dtype=torch.bfloat16), bt=torch.zeros(2, 4, dtype=torch.int32),
+             lens=torch.ones(2, dtype=torch.int32))
+    t.update(kw)
+    return t
+
+
+@pytest.mark.parametrize("kw,msg", [
+    ({"q": torch.zeros(2, 9, 32)}, "head_dim must be 64"),
+    ({"k": torch.zeros(64, 3, 32, dtype=torch.bfloat16), "v": torch.zeros(64, 3, 32, dtype=torch.bfloat16)},
+     "head_dim 32 differs"),
+    ({"v": torch.zeros(64, 3, 64)}, "v_cache must be a contiguous bf16"),
+    ({"v": torch.zeros(32, 3, 64, dtype=torch.bfloat16)}, "differ in shape"),
+    ({"bt": torch.zeros(3, 4, dtype=torch.int32)}, "one row per query row"),
+    ({"lens": torch.ones(2, dtype=torch.int64)}, "context_lens"),
+    ({"k": torch.zeros(64, 3, 64, dtype=torch.bfloat16, device="meta")}, "every operand must be on q's device"),
+    ({"bt": torch.zeros(2, 4, dtype=torch.int32, device="meta")}, "every operand must be on q's device"),
+    ({"k": torch.zeros(64 * 3 * 64 + 1, dtype=torch.bfloat16)[1:].view(64, 3, 64)}, "16-byte boundary"),
+    ({}, "no CPU path"),
+])
+def test_decode_attention_rejects_bad_operands(kw, msg):
+    """Every operand is checked before the kernel sees a pointer: a cache with another
+    head size, a tensor on another device or on the host, a view off a 16-byte boundary."""
+    from pagedbatch_amd.attention import decode_attention
+
+    t = _attn_tensors(**kw)
+    with pytest.raises(ValueError, match=msg):
+        decode_attention(t["q"], t["k"], t["v"], t["bt"], t["lens"], block_size=16, max_context=64)
