@@ -118,6 +118,9 @@ __device__ __forceinline__ uint32_t bcast_u32(uint32_t v, int lane) {
 __device__ __forceinline__ float bcast_f32(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
+// a value the program knows to be the same in every lane (an LDS word all lanes read, for
+// example), made visibly wave-uniform: branches on it become scalar branches
+__device__ __forceinline__ uint32_t uni_u32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 __device__ __forceinline__ double bcast_f64(double v, int lane) {
   const uint64_t b = (uint64_t)__double_as_longlong(v);
   const uint32_t lo = bcast_u32((uint32_t)b, lane), hi = bcast_u32((uint32_t)(b >> 32), lane);
@@ -465,7 +468,6 @@ struct __align__(16) Smem {
   double red_d2[NWAVE];
   float red_f[NWAVE];
   int red_i[2 * NWAVE];
-  uint32_t nan_cnt;              // 16-bit rows: elements in the NaN / inf raw blocks
 
   int sel_jstar, sel_rank, sel_index;
   TieGroup spec[2];              // 16-bit rows: cutoff and guessed draw, searched side by side
@@ -1646,8 +1648,8 @@ __device__ __forceinline__ int select_tied16(const Src& src, Smem& s, uint32_t l
     // lo - 0x8000.., negative ones to raws 0xffff - hi ..)
     if (lo >= 0x8000u || hi < 0x8000u)
       return select_index_reg16<false>(src, s, lo >= 0x8000u ? lo - 0x8000u : 0xffffu - hi, hi - lo, rank, out, b);
-    // a range taking in both -0 and +0 (rare): the general selection on ords
-    return select_index<DT>(src, s, [=](uint32_t raw) { return ord16u(raw) - lo <= hi - lo; }, rank);
+    // a range taking in both -0 and +0 (rare): the same selection on unfolded ords
+    return select_index_reg16<true>(src, s, lo, hi - lo, rank, out, b);
   } else {
     return select_index<DT>(src, s, [=](uint32_t raw) { return ord16u(raw) - lo <= hi - lo; }, rank);
   }
@@ -1658,12 +1660,10 @@ __device__ __forceinline__ void hist_clear(Smem& s) {
   u4* h4 = (u4*)s.hist;
 #pragma unroll
   for (int i = 0; i < HIST_WORDS / 4 / NT; ++i) h4[i * NT + threadIdx.x] = (u4){0u, 0u, 0u, 0u};
-  if (threadIdx.x == 0) s.nan_cnt = 0u;
 }
 
 // group counts: thread t sums raws [128t, 128t + 128) (half a group, sixteen 16-byte LDS
-// reads, rotated by lane so that a wave's reads spread over the banks); the elements of the
-// top raw blocks of each sign (inf / NaN of the 16-bit types) also go into s.nan_cnt
+// reads, rotated by lane so that a wave's reads spread over the banks)
 template <int DT>
 __device__ __forceinline__ void hist_group_counts(Smem& s) {
   const int l = lane_id();
@@ -1678,8 +1678,6 @@ __device__ __forceinline__ void hist_group_counts(Smem& s) {
     c3 = add_u16_pair(qv.w, c3);
   }
   uint32_t c = (c0 + c1) + (c2 + c3);
-  const uint32_t r0 = threadIdx.x * 128u, inf_raw = DT == PBS_DTYPE_F16 ? 0x7c00u : 0x7f80u;
-  if ((r0 & 0x7fffu) >= (inf_raw & ~127u) && c) atomicAdd(&s.nan_cnt, c);
   c += dpp<0xb1>(c, 0u);  // quad_perm [1,0,3,2]: the other half of the block
   if ((l & 1) == 0) {
     const uint32_t blk = threadIdx.x >> 1;
@@ -1687,78 +1685,18 @@ __device__ __forceinline__ void hist_group_counts(Smem& s) {
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// 16-bit stochastic row
-// ---------------------------------------------------------------------------------------
+// The tail of a 16-bit row once the histogram is complete and the row maximum m is known:
+// group counts, the k-th element by counts (top-k rows), group masses from the k-th
+// element's group up, prefix tables, the searches (waves 0 and 1) and the selection.
+// Returns false when the general path must take the row (a u16 counter wrapped).
 template <int DT, class Src>
-__device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, int b, float T, int kk, float p,
-                                             float u) {
-  constexpr int EPV = DTraits<DT>::EPV;
+__device__ __forceinline__ bool tail16(const KArgs& a, Smem& s, Src& src, int b, const Divider& dv, float m, int kk,
+                                       float p, float u) {
   const int V = a.vocab;
   const int l = lane_id(), wv = wave_id();
 
-  // stream: the histogram. It is cleared while the first loads are in flight; the
-  // barrier orders LDS only.
-  hist_clear(s);
-  lds_barrier();
-  src.stream([&](int, const u4& q, int base, bool vvalid) {
-    if constexpr (Src::kVector) {
-      if (vvalid) {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) hist_add_pair(s, q[d]);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPV; ++e)
-        if (elem_valid(src, vvalid, base + e)) hist_add_one(s, elem_raw<DT>(q, e));
-    }
-  });
-  __syncthreads();
-
   hist_group_counts<DT>(s);
   __syncthreads();
-
-  // Every wave checks the total (a u16 counter wraps only if one value occurs more than
-  // 65535 times: the general path takes such rows) and NaN (multinomial raises on it,
-  // sampling.py:27), and finds the row maximum from the highest non-empty ord. The three
-  // are independent: all loads first, the tests after the maximum.
-  uint32_t omax;
-  uint32_t total, nan;
-  {
-    uint32_t gc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) gc[i] = s.gcount[4 * l + i];
-    const uint32_t inf_raw = DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
-    nan = s.nan_cnt - hist_count_raw(s, inf_raw) - hist_count_raw(s, inf_raw | 0x8000u);
-    total = wsum_u32((gc[0] + gc[1]) + (gc[2] + gc[3]));
-    uint32_t nz = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) nz |= (gc[i] ? 1u : 0u) << i;
-    const uint64_t any = ballot(nz != 0u);
-    // (empty only if counters wrapped, which the total test below catches)
-    const int L = any ? 63 - __clzll((unsigned long long)any) : 0;
-    const uint32_t g = 4u * (uint32_t)L + (31u - __clz(bcast_u32(nz, L) | 1u));
-    uint32_t n4[4];
-    counts4(s, g * 256u + 4u * (uint32_t)l, n4);
-    uint32_t top = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) top = n4[i] ? (uint32_t)i + 1u : top;
-    const uint64_t any2 = ballot(top != 0u);
-    const int L2 = any2 ? 63 - __clzll((unsigned long long)any2) : 0;
-    omax = g * 256u + 4u * (uint32_t)L2 + max(bcast_u32(top, L2), 1u) - 1u;
-  }
-  if (total != (uint32_t)V) return false;
-  if (nan) {
-    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NAN, NAN);
-    return true;
-  }
-  Divider dv;
-  dv.init(T);
-  const float m = scaled16<DT>(omax, dv);
-  if (!(m > -INFINITY && m < INFINITY)) {
-    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NONFINITE, m);
-    return true;
-  }
 
   // top-k (sampling.py:15-17): the k-th element by counts; only its tie group and the
   // groups above it (K) need masses
@@ -1842,6 +1780,83 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
   const int tok = select_tied16<DT>(src, s, s.res_lo, s.res_hi, s.res_rank, a.out_info ? nullptr : &a, b);
   if (tok != SEL_WRITTEN && threadIdx.x == 0) write_info(a, b, tok < 0 ? 0 : tok, PBS_ROW_OK, st);
   return true;
+}
+
+// ---------------------------------------------------------------------------------------
+// 16-bit stochastic row
+//
+// The stream builds the histogram and every thread's largest and smallest ord (packed u16
+// max / min), so the row maximum and the NaN test are known at the stream's barrier, with
+// no pass over the histogram for them.
+// ---------------------------------------------------------------------------------------
+template <int DT, class Src>
+__device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, int b, float T, int kk, float p,
+                                             float u) {
+  constexpr int EPV = DTraits<DT>::EPV;
+  const int V = a.vocab;
+  const int l = lane_id(), wv = wave_id();
+  Divider dv;
+  dv.init(T);  // (its division overlaps the first loads)
+
+  // stream: the histogram and the thread's ord range (packed u16 max / min of the unfolded
+  // ords). The histogram is cleared while the first loads are in flight; the barrier
+  // orders LDS only.
+  hist_clear(s);
+  lds_barrier();
+  uint32_t omx = 0u, omn = 0xffffffffu;
+  src.stream([&](int, const u4& q, int base, bool vvalid) {
+    if constexpr (Src::kVector) {
+      if (vvalid) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          hist_add_pair(s, q[d]);
+          const uint32_t o2 = ord16_pair(q[d]);
+          omx = pk_max_u16(omx, o2);
+          omn = pk_min_u16(omn, o2);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e)
+        if (elem_valid(src, vvalid, base + e)) {
+          const uint32_t raw = elem_raw<DT>(q, e);
+          hist_add_one(s, raw);
+          const uint32_t o = ord16u(raw);
+          omx = pk_max_u16(omx, o | (o << 16));
+          omn = pk_min_u16(omn, o | (o << 16));
+        }
+    }
+  });
+  {
+    const uint32_t mx = wmax_u32(max(omx & 0xffffu, omx >> 16));
+    const uint32_t mn = wmin_u32(min(omn & 0xffffu, omn >> 16));
+    if (l == 0) {
+      s.red_i[wv] = (int)mx;
+      s.red_i[NWAVE + wv] = (int)mn;
+    }
+  }
+  __syncthreads();
+  uint32_t omax = 0u, omin = 0xffffu;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    omax = max(omax, (uint32_t)s.red_i[w]);
+    omin = min(omin, (uint32_t)s.red_i[NWAVE + w]);
+  }
+  omax = uni_u32(omax);
+  omin = uni_u32(omin);
+  // NaN (multinomial raises on it, sampling.py:27): ords above +inf or below -inf
+  if (omax > ord16u(DT == PBS_DTYPE_BF16 ? 0x7f80u : 0x7c00u) ||
+      omin < ord16u(DT == PBS_DTYPE_BF16 ? 0xff80u : 0xfc00u)) {
+    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NAN, NAN);
+    return true;
+  }
+  const float m = scaled16<DT>(omax, dv);
+  if (!(m > -INFINITY && m < INFINITY)) {
+    if (threadIdx.x == 0) write_error(a, b, PBS_ROW_NONFINITE, m);
+    return true;
+  }
+
+  return tail16<DT>(a, s, src, b, dv, m, kk, p, u);
 }
 
 // ---------------------------------------------------------------------------------------
