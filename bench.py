@@ -311,13 +311,21 @@ def main():
     dcode = _TORCH_DTYPE[w.logits.dtype]
     stream = torch.cuda.current_stream(dev)
 
+    # a step whose rows are all greedy goes to the argmax kernel, as sample() routes it
+    greedy = all(t == 0 for t in w.temperature)
+    entry = "pbs_argmax" if greedy else "pbs_sample"
+
     def launch(i):
         x = bufs[i % copies]
         sp = torch.cuda.current_stream(dev).cuda_stream  # the capture stream inside a graph capture
-        rc = lib.pbs_sample(x.data_ptr(), dcode, rows, rows, vocab, vocab, None, T.data_ptr(), K.data_ptr(),
-                            P.data_ptr(), U.data_ptr(), tok.data_ptr(), st.data_ptr(), None, 0, sp)
+        if greedy:
+            rc = lib.pbs_argmax(x.data_ptr(), dcode, rows, rows, vocab, vocab, None, tok.data_ptr(), st.data_ptr(),
+                                sp)
+        else:
+            rc = lib.pbs_sample(x.data_ptr(), dcode, rows, rows, vocab, vocab, None, T.data_ptr(), K.data_ptr(),
+                                P.data_ptr(), U.data_ptr(), tok.data_ptr(), st.data_ptr(), None, 0, sp)
         if rc != 0:
-            raise RuntimeError(f"pbs_sample failed: {_lib.last_error(lib)}")
+            raise RuntimeError(f"{entry} failed: {_lib.last_error(lib)}")
 
     print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
     for i in range(args.warmup):
@@ -410,6 +418,7 @@ def main():
         "data": "synthetic (seeded logits recipe, see pagedbatch_amd/workloads.py)",
         "config": {"workload": w.name, "rows": rows, "vocab": vocab, "logits_dtype": str(w.logits.dtype),
                    "buffers_rotated": copies, "parallelism": "single GPU"},
+        "entry_point": entry,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_note, "algorithmic_bytes_per_launch": alg_bytes},

@@ -135,6 +135,20 @@ int pbs_sample_debug(const void* logits, int dtype, int64_t n_logit_rows, int64_
                      int32_t* out_token, int32_t* out_status, float* out_probs, uint8_t* out_kept,
                      pbs_row_info* out_info, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Greedy-only steps: the token of every output row is the index of the first maximum of
+ * its logits row, or of the first NaN if the row holds one (torch.argmax,
+ * pagedbatch/sampling.py:12-13, reached through the per-row loop at
+ * pagedbatch/engine.py:133-139 when every sampled row has temperature 0). Tokens are
+ * identical to pbs_sample's with temperature 0 on every row; only a row_map entry outside
+ * [0, n_logit_rows) gives a status other than PBS_ROW_OK (PBS_ROW_BAD_PARAM, token 0).
+ * The kernel keeps no histogram, so it needs none of pbs_sample's per-row parameters and
+ * streams the logits at a higher rate.
+ */
+int pbs_argmax(const void* logits, int dtype, int64_t n_logit_rows, int64_t rows, int64_t vocab,
+               int64_t row_stride, const int32_t* row_map, int32_t* out_token, int32_t* out_status,
+               void* stream);
+
 /* finish reasons written by pbs_finish_reasons */
 enum {
   PBS_FINISH_NONE = 0,

@@ -40,7 +40,7 @@ ATTN_SYMBOLS = ("pba_decode_attention",)
 
 # the C symbols include/pbsample.h declares, in declaration order
 SYMBOLS = ("pbs_abi_version", "pbs_last_error", "pbs_workspace_bytes", "pbs_sample", "pbs_sample_debug",
-           "pbs_finish_reasons")
+           "pbs_argmax", "pbs_finish_reasons")
 
 # layout of pbs_row_info
 ROW_INFO_DTYPE = np.dtype(
@@ -117,6 +117,19 @@ def load(path: str | None = None):
             _c.c_void_p,  # out_info
             _c.c_void_p,  # workspace
             _c.c_size_t,  # workspace_bytes
+            _c.c_void_p,  # stream
+        ]
+        lib.pbs_argmax.restype = _c.c_int
+        lib.pbs_argmax.argtypes = [
+            _c.c_void_p,  # logits
+            _c.c_int,  # dtype
+            _c.c_int64,  # n_logit_rows
+            _c.c_int64,  # rows
+            _c.c_int64,  # vocab
+            _c.c_int64,  # row_stride
+            _c.c_void_p,  # row_map
+            _c.c_void_p,  # out_token
+            _c.c_void_p,  # out_status
             _c.c_void_p,  # stream
         ]
         lib.pbs_finish_reasons.restype = _c.c_int

@@ -68,6 +68,9 @@ struct KArgs {
 // one launch of the sampler for logits type DT (defined with the kernels)
 template <int DT>
 int launch_dt(const KArgs& a, int64_t rows, bool vec, hipStream_t stream);
+// one launch of the all-greedy kernel (argmax of every row) for logits type DT
+template <int DT>
+int launch_argmax(const KArgs& a, int64_t rows, bool vec, hipStream_t stream);
 
 // error reporting shared by the translation units (pbs_last_error reads it)
 int report_error(int code, const char* msg);
@@ -2928,10 +2931,160 @@ int launch_dt(const KArgs& a, int64_t rows, bool vec, hipStream_t stream) {
   return PBS_OK;
 }
 
+// ---------------------------------------------------------------------------------------
+// All-greedy steps: torch.argmax of every row (sampling.py:12-13), first NaN if any, else
+// the first maximum. Pure streaming: no histogram, so the workgroups are small (256
+// threads, a few dozen bytes of LDS) and several share a CU. Each thread keeps eight
+// 16-byte loads in flight (two groups of four, the next group issued before the current
+// one is read) and does per-vector work only: the vector's maximum, one compare with the
+// running best, and a copy of the best vector, whose first element equal to the maximum is
+// resolved once at the end. A NaN is only flagged on the way (one unordered compare per
+// pair); a row that holds one is scanned again for its first NaN.
+// ---------------------------------------------------------------------------------------
+constexpr int NT_AM = 256;
+constexpr int G_AM = 4;
+
+template <int DT>
+__device__ __forceinline__ float vec_max(const u4& q, bool& nan) {
+  constexpr int EPV = DTraits<DT>::EPV;
+  float e[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) e[i] = raw_to_float<DT>(elem_raw<DT>(q, i));
+  bool n = false;
+#pragma unroll
+  for (int i = 0; i < EPV; i += 2) n |= __builtin_isunordered(e[i], e[i + 1]);
+  nan |= n;
+#pragma unroll
+  for (int w = 1; w < EPV; w *= 2) {
+#pragma unroll
+    for (int i = 0; i + w < EPV; i += 2 * w) e[i] = fmaxf(e[i], e[i + w]);
+  }
+  return e[0];
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(NT_AM) void k_argmax(KArgs a) {
+  constexpr int EPV = DTraits<DT>::EPV;
+  constexpr size_t ELT = DTraits<DT>::B16 ? 2 : 4;
+  __shared__ float red_v[NT_AM / 64];
+  __shared__ int red_i[NT_AM / 64];
+  const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t lrow = a.row_map ? (int64_t)a.row_map[b] : (int64_t)b;
+  if (!(lrow >= 0 && lrow < a.n_logit_rows)) {
+    if (t == 0) {
+      a.out_token[b] = 0;
+      a.out_status[b] = PBS_ROW_BAD_PARAM;
+    }
+    return;
+  }
+  const uint8_t* row = (const uint8_t*)a.logits + (size_t)lrow * (size_t)a.row_stride * ELT;
+  auto elem = [&](int i) {
+    return DTraits<DT>::B16 ? raw_to_float<DT>(((const uint16_t*)row)[i]) : raw_to_float<DT>(((const uint32_t*)row)[i]);
+  };
+  // the thread's candidate: its largest value (NaN aside) and the lowest index holding it;
+  // INT32_MAX when every value it saw was -inf or NaN
+  float bv = -INFINITY;
+  int bi = INT32_MAX;
+  bool nan = false;
+  if constexpr (VEC) {
+    const int nvec = a.nvec;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, nvec * 16, 0x00020000);
+    // the whole offset goes in the VGPR operand, which the buffer's range check covers
+    auto ld = [&](int j) {
+      return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(j * NT_AM + t) * 16u, 0, 2));
+    };
+    const int nch = (nvec + NT_AM - 1) / NT_AM;
+    int bvec = -1;
+    u4 bq = {0u, 0u, 0u, 0u};
+    u4 cur[G_AM], nxt[G_AM];
+#pragma unroll
+    for (int k = 0; k < G_AM; ++k) cur[k] = ld(k);
+    for (int j0 = 0; j0 < nch; j0 += G_AM) {
+#pragma unroll
+      for (int k = 0; k < G_AM; ++k) nxt[k] = ld(j0 + G_AM + k);  // past the row: zeros, never read
+#pragma unroll
+      for (int k = 0; k < G_AM; ++k) {
+        const int v = (j0 + k) * NT_AM + t;
+        if (v < nvec) {
+          // vectors reach a thread in increasing index order: strict > keeps the first
+          const float m = vec_max<DT>(cur[k], nan);
+          const bool up = m > bv;
+          bv = up ? m : bv;
+          bvec = up ? v : bvec;
+          bq = up ? cur[k] : bq;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < G_AM; ++k) cur[k] = nxt[k];
+    }
+    if (bvec >= 0) {
+      int e = EPV - 1;
+#pragma unroll
+      for (int i = EPV - 2; i >= 0; --i) e = (raw_to_float<DT>(elem_raw<DT>(bq, i)) == bv) ? i : e;
+      bi = bvec * EPV + e;
+    }
+  } else {
+    for (int i = t; i < a.vocab; i += NT_AM) {
+      const float v = elem(i);
+      nan |= (v != v);
+      const bool up = v > bv;
+      bv = up ? v : bv;
+      bi = up ? i : bi;
+    }
+  }
+  // a row holding a NaN: its first NaN, found by a second pass
+  if (__syncthreads_or(nan)) {
+    int ni = INT32_MAX;
+    for (int i = t; i < a.vocab; i += NT_AM) {
+      if (elem(i) != elem(i)) {
+        ni = i;
+        break;
+      }
+    }
+    bv = ni != INT32_MAX ? INFINITY : -INFINITY;
+    bi = ni;
+  }
+  // block reduction: the largest value, lowest index on ties
+  const float wm = wmax_f32(bv);
+  const int wi = wmin_i32(bv == wm ? bi : INT32_MAX);
+  const int w = t >> 6;
+  if ((t & 63) == 0) {
+    red_v[w] = wm;
+    red_i[w] = wi;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float v = red_v[0];
+    int i = red_i[0];
+#pragma unroll
+    for (int k = 1; k < NT_AM / 64; ++k) {
+      if (red_v[k] > v || (red_v[k] == v && red_i[k] < i)) {
+        v = red_v[k];
+        i = red_i[k];
+      }
+    }
+    // every value -inf (no candidate anywhere): index 0, as torch.argmax gives
+    a.out_token[b] = i == INT32_MAX ? 0 : i;
+    a.out_status[b] = PBS_ROW_OK;
+  }
+}
+
+template <int DT>
+int launch_argmax(const KArgs& a, int64_t rows, bool vec, hipStream_t stream) {
+  const dim3 grid((unsigned)rows), block(NT_AM);
+  if (vec) hipLaunchKernelGGL((k_argmax<DT, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((k_argmax<DT, false>), grid, block, 0, stream, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return report_errorf(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return PBS_OK;
+}
+
 }  // namespace pbs
 
 #if defined(PBS_TU_DTYPE)
 template int pbs::launch_dt<PBS_TU_DTYPE>(const pbs::KArgs&, int64_t, bool, hipStream_t);
+template int pbs::launch_argmax<PBS_TU_DTYPE>(const pbs::KArgs&, int64_t, bool, hipStream_t);
 #endif
 #endif  // PBS_WANT_KERNELS
 
@@ -3081,6 +3234,43 @@ int pbs_sample_debug(const void* logits, int dtype, int64_t n_logit_rows, int64_
   (void)workspace_bytes;
   return sample_impl(logits, dtype, n_logit_rows, rows, vocab, row_stride, row_map, temperature, top_k, top_p,
                      uniform, out_token, out_status, out_probs, out_kept, out_info, stream);
+}
+
+int pbs_argmax(const void* logits, int dtype, int64_t n_logit_rows, int64_t rows, int64_t vocab,
+               int64_t row_stride, const int32_t* row_map, int32_t* out_token, int32_t* out_status,
+               void* stream) {
+  g_last_error[0] = '\0';
+  if (dtype != PBS_DTYPE_F32 && dtype != PBS_DTYPE_F16 && dtype != PBS_DTYPE_BF16)
+    return fail(PBS_ERR_UNSUPPORTED_DTYPE, "unsupported dtype code %d", dtype);
+  if (rows < 0 || n_logit_rows < 0) return fail(PBS_ERR_INVALID_ARGUMENT, "negative row count");
+  if (rows == 0) return PBS_OK;
+  if (vocab < 1 || vocab > (int64_t(1) << 27))
+    return fail(PBS_ERR_INVALID_ARGUMENT, "vocab %lld outside [1, 2^27]", (long long)vocab);
+  if (rows > INT32_MAX) return fail(PBS_ERR_INVALID_ARGUMENT, "too many rows");
+  if (row_stride < vocab)
+    return fail(PBS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %lld", (long long)row_stride, (long long)vocab);
+  if (!logits || !out_token || !out_status) return fail(PBS_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (!row_map && n_logit_rows < rows)
+    return fail(PBS_ERR_INVALID_ARGUMENT, "rows %lld > n_logit_rows %lld without row_map", (long long)rows,
+                (long long)n_logit_rows);
+  const int elt = dtype == PBS_DTYPE_F32 ? 4 : 2;
+  const int epv = 16 / elt;
+  const bool vec = ((uintptr_t)logits % 16 == 0) && ((row_stride * elt) % 16 == 0) && (vocab % epv == 0);
+  pbs::KArgs a = {};
+  a.logits = logits;
+  a.n_logit_rows = n_logit_rows;
+  a.row_stride = row_stride;
+  a.vocab = (int)vocab;
+  a.nvec = (int)((vocab + epv - 1) / epv);
+  a.row_map = row_map;
+  a.out_token = out_token;
+  a.out_status = out_status;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case PBS_DTYPE_F32: return pbs::launch_argmax<PBS_DTYPE_F32>(a, rows, vec, st);
+    case PBS_DTYPE_F16: return pbs::launch_argmax<PBS_DTYPE_F16>(a, rows, vec, st);
+    default: return pbs::launch_argmax<PBS_DTYPE_BF16>(a, rows, vec, st);
+  }
 }
 
 int pbs_finish_reasons(const int32_t* tokens, int64_t rows, int32_t eos_token_id, const uint8_t* ignore_eos,

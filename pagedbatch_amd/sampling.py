@@ -131,6 +131,14 @@ def _pack(n, temperature, top_k, top_p, uniform, row_map, vocab) -> np.ndarray:
     return h
 
 
+def _all_greedy(h: np.ndarray) -> bool:
+    """True when every row of a packed block is greedy with valid parameters: then
+    ``pbs_argmax`` returns exactly what ``pbs_sample`` would (it checks only the row map)."""
+    t = h[_IN_T].view(np.float32)
+    p = h[_IN_P].view(np.float32)
+    return bool((t == 0).all() and (h[_IN_K] >= 0).all() and ((p > 0) & (p <= 1)).all())
+
+
 def _stage_params(bufs: _Buffers, h: np.ndarray, n: int) -> None:
     cap = bufs.cap
     for i in range(5):
@@ -177,8 +185,10 @@ def _raise_for_status(status: np.ndarray, temperature: np.ndarray | None = None)
     raise RuntimeError(_BAD_PROBS)
 
 
-def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, finish=None, timing=None):
-    """Copy the staged params to the device and call the C ABI; with ``finish`` (eos id,
+def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, finish=None, timing=None,
+            greedy: bool = False):
+    """Copy the staged params to the device and call the C ABI (``pbs_argmax`` when
+    ``greedy``: every row greedy with valid parameters); with ``finish`` (eos id,
     max_model_len, number of stop ids) also the stop check, on the sampler's device tokens.
     Returns host tokens, statuses and reasons (None without ``finish``) plus the device
     diagnostics of a debug call."""
@@ -214,6 +224,8 @@ def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, fi
         kept = torch.empty((n, V), dtype=torch.uint8, device=logits.device)
         info = torch.empty(n * _lib.ROW_INFO_DTYPE.itemsize, dtype=torch.uint8, device=logits.device)
         rc = lib.pbs_sample_debug(*args, probs.data_ptr(), kept.data_ptr(), info.data_ptr(), None, 0, sp)
+    elif greedy:
+        rc = lib.pbs_argmax(*args[:7], out_tok, out_st, sp)
     else:
         rc = lib.pbs_sample(*args, None, 0, sp)
     if rc != _lib.OK:
@@ -222,7 +234,8 @@ def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, fi
             raise ValueError(msg)
         if rc == _lib.ERR_UNSUPPORTED_DTYPE:
             raise TypeError(msg)
-        raise SamplerError(f"pbs_sample failed ({rc}): {msg}")
+        what = "pbs_argmax" if greedy and not debug else "pbs_sample"
+        raise SamplerError(f"{what} failed ({rc}): {msg}")
     nout = 2
     if finish is not None:
         eos, max_model_len, nstop = finish
@@ -324,7 +337,7 @@ def _sample(logits, params, generators, rows, finish_rules=None, eos_token_id=No
         if timing is not None:
             timing["pack"] = time.perf_counter()
         tokens, status, reasons, _, _, _ = _launch(logits, n, rows is not None, False, bufs, finish=fin,
-                                                   timing=timing)
+                                                   timing=timing, greedy=_all_greedy(h))
     _raise_for_status(status, t)
     toks = tokens.tolist()
     if finish_rules is None:
@@ -380,7 +393,8 @@ def sample_arrays(logits: torch.Tensor, temperature, top_k, top_p, uniform, row_
     with bufs.lock:
         bufs.ensure(n)
         _stage_params(bufs, h, n)
-        tokens, status, _, probs, kept, info = _launch(logits, n, row_map is not None, debug, bufs)
+        tokens, status, _, probs, kept, info = _launch(logits, n, row_map is not None, debug, bufs,
+                                                       greedy=not debug and _all_greedy(h))
     if check:
         _raise_for_status(status, np.asarray(temperature, dtype=np.float64))
     if not debug:

@@ -233,6 +233,44 @@ def test_abi_zero_rows_is_a_no_op():
     assert _call(lib, rows=0) == _lib.OK
 
 
+def _argmax_call(lib, **kw):
+    a = dict(logits=1 << 20, dtype=_lib.DTYPE_BF16, n_rows=4, rows=4, vocab=1000, stride=1000, row_map=None,
+             tok=1 << 20, st=1 << 20)
+    a.update(kw)
+    return lib.pbs_argmax(a["logits"], a["dtype"], a["n_rows"], a["rows"], a["vocab"], a["stride"], a["row_map"],
+                          a["tok"], a["st"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    ({"dtype": 3}, _lib.ERR_UNSUPPORTED_DTYPE, "unsupported dtype"),
+    ({"n_rows": -1}, _lib.ERR_INVALID_ARGUMENT, "negative"),
+    ({"vocab": 0}, _lib.ERR_INVALID_ARGUMENT, "vocab"),
+    ({"stride": 10}, _lib.ERR_INVALID_ARGUMENT, "row_stride"),
+    ({"tok": None}, _lib.ERR_INVALID_ARGUMENT, "null"),
+    ({"st": None}, _lib.ERR_INVALID_ARGUMENT, "null"),
+    ({"rows": 5}, _lib.ERR_INVALID_ARGUMENT, "n_logit_rows"),
+])
+def test_argmax_abi_rejects_bad_arguments(kw, code, msg):
+    lib = _lib.load()
+    assert _argmax_call(lib, **kw) == code
+    assert msg in _lib.last_error(lib)
+    assert _argmax_call(lib, rows=0) == _lib.OK
+
+
+def test_all_greedy_routing():
+    """The Python surface sends a block to pbs_argmax only when every row is greedy with
+    parameters pbs_sample would accept, so both entry points give the same result."""
+    def block(t, k, p):
+        return smp._pack(len(t), t, k, p, [0.5] * len(t), None, 1000)
+
+    assert smp._all_greedy(block([0.0, -0.0], [0, 5], [1.0, 0.3]))
+    assert not smp._all_greedy(block([0.0, 1.0], [0, 0], [1.0, 1.0]))
+    assert not smp._all_greedy(block([0.0, 0.0], [0, -1], [1.0, 1.0]))
+    assert not smp._all_greedy(block([0.0], [0], [0.0]))
+    assert not smp._all_greedy(block([0.0], [0], [1e-50]))  # zero in float32
+    assert not smp._all_greedy(block([0.0], [0], [float("nan")]))
+
+
 def test_debug_outputs_need_info():
     lib = _lib.load()
     rc = lib.pbs_sample_debug(1 << 20, _lib.DTYPE_F32, 1, 1, 10, 10, None, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
