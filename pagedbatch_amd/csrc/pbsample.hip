@@ -417,6 +417,26 @@ struct UnitDivider {
   __device__ __forceinline__ float operator()(float a) const { return a; }
 };
 
+// The four quotients of one 16-byte vector of fp32 values. Divider: the FMA sequence for
+// all four, then the general division behind one wave-uniform branch, taken only when some
+// lane holds an element the FMA sequence does not cover (no per-element branches).
+__device__ __forceinline__ void div4(const UnitDivider&, const u4& q, float x[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(q[e]);
+}
+__device__ __forceinline__ void div4(const Divider& dv, const u4& q, float x[4]) {
+  bool ok = true;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = dv.fma_seq(__uint_as_float(q[e]));
+    ok = ok && dv.safe_exp((int)((q[e] >> 23) & 0xffu));
+  }
+  if (__builtin_expect(__any(!ok), 0)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = dv(__uint_as_float(q[e]));
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // kernel arguments and per-row shared state
 // ---------------------------------------------------------------------------------------
@@ -2087,6 +2107,13 @@ constexpr double FIXQ = 0x1p-38;               // fixed-point weight unit
 __device__ __forceinline__ float wexp(float x, float m) {
   return (x > -INFINITY) ? __builtin_amdgcn_exp2f((x - m) * LOG2E_F) : 0.0f;
 }
+// the same weight for x that is not NaN, without the test (x = -inf gives exp2(-inf) = 0)
+__device__ __forceinline__ float wexp_num(float x, float m) { return __builtin_amdgcn_exp2f((x - m) * LOG2E_F); }
+// ord32(x) for x that is not NaN: x + 0 turns -0 into +0 and leaves every other value alone
+__device__ __forceinline__ uint32_t ord32_num(float x) {
+  const uint32_t b = __float_as_uint(x + 0.0f);
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
 // floor(w * 2^38) for 0 <= w < 2: at most 2^39, so 2^14 of them sum exactly in a double
 __device__ __forceinline__ uint64_t fixq(float w) {
   return (uint64_t)((double)w * 0x1p38);
@@ -2231,25 +2258,59 @@ __device__ __forceinline__ bool gather_bins(const Src& src, Smem& s, uint64_t* L
     float part[NW];
 #pragma unroll
     for (int r = 0; r < NW; ++r) part[r] = 0.0f;
+    if constexpr (Src::kVector) {
+      // Straight-line work per element (no NaN reaches this pass); the appends sit behind
+      // one ballot per vector, which is empty for nearly every vector.
+      float xs[4];
+      div4(dv, q, xs);
+      uint32_t key[4];
+      bool in[4];
+      bool any = false;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x = x_at<DT>(dv, q, e);
-      const uint32_t key = ord32(x);
-      const uint32_t o = key >> 16;
-      const bool ok = elem_valid(src, vvalid, base + e);
-      const float w = ok ? wexp(x, m) : 0.0f;
-      bool in = false;
+      for (int e = 0; e < 4; ++e) {
+        key[e] = ord32_num(xs[e]);
+        const uint32_t o = key[e] >> 16;
+        const float w = vvalid ? wexp_num(xs[e], m) : 0.0f;
+        bool hit = false;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) {
-        part[r] += (o > hi[r]) ? w : 0.0f;
-        in = in || (o - lo[r] <= hi[r] - lo[r]);
+        for (int r = 0; r < NW; ++r) {
+          part[r] += (o > hi[r]) ? w : 0.0f;
+          hit = hit || (o - lo[r] <= hi[r] - lo[r]);
+        }
+        in[e] = vvalid && hit;
+        any = any || in[e];
       }
-      const uint64_t bal = ballot(ok && in);
-      if (bal) {
-        const uint32_t slot = wn + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        if (ok && in && slot < SEG) seg[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
-        wn += (uint32_t)__popcll(bal);
+      if (ballot(any)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint64_t bal = ballot(in[e]);
+          const uint32_t slot = wn + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          if (in[e] && slot < SEG) seg[slot] = ((uint64_t)(~key[e]) << 32) | (uint32_t)(base + e);
+          wn += (uint32_t)__popcll(bal);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = x_at<DT>(dv, q, e);
+        const uint32_t key = ord32(x);
+        const uint32_t o = key >> 16;
+        const bool ok = elem_valid(src, vvalid, base + e);
+        const float w = ok ? wexp(x, m) : 0.0f;
+        bool in = false;
+#pragma unroll
+        for (int r = 0; r < NW; ++r) {
+          part[r] += (o > hi[r]) ? w : 0.0f;
+          in = in || (o - lo[r] <= hi[r] - lo[r]);
+        }
+        const uint64_t bal = ballot(ok && in);
+        if (bal) {
+          const uint32_t slot = wn + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          if (ok && in && slot < SEG) seg[slot] = ((uint64_t)(~key) << 32) | (uint32_t)(base + e);
+          wn += (uint32_t)__popcll(bal);
+        }
       }
     }
 #pragma unroll
@@ -2450,16 +2511,31 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   int nan = 0;
   src0.stream([&](int, const u4& q, int base, bool vvalid) {
     float xs[4];
-    float cm = -INFINITY;
+    if constexpr (Src0::kVector) {
+      // whole vectors are valid or not: one branch per vector, the bins of two values
+      // (top 16 bits, -0 folded by x + 0) packed into one word for hist_add_pair
+      div4(dv, q, xs);
+      if (vvalid) {
+        uint32_t bb[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool ok = elem_valid(src0, vvalid, base + e);
-      const float x = x_at<DT>(dv, q, e);
-      if (ok) hist_add_one(s, bin_raw32(x));
-      xs[e] = ok ? x : -INFINITY;
-      nan |= (xs[e] != xs[e]) ? 1 : 0;
-      cm = fmaxf(cm, xs[e]);
+        for (int e = 0; e < 4; ++e) bb[e] = __float_as_uint(xs[e] + 0.0f);
+        hist_add_pair(s, (bb[1] & 0xffff0000u) | (bb[0] >> 16));
+        hist_add_pair(s, (bb[3] & 0xffff0000u) | (bb[2] >> 16));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xs[e] = -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = elem_valid(src0, vvalid, base + e);
+        const float x = x_at<DT>(dv, q, e);
+        if (ok) hist_add_one(s, bin_raw32(x));
+        xs[e] = ok ? x : -INFINITY;
+      }
     }
+    nan |= (__builtin_isunordered(xs[0], xs[1]) || __builtin_isunordered(xs[2], xs[3])) ? 1 : 0;
+    const float cm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
     const float mn = fmaxf(xmax, cm);
     const float mr = (mn > -INFINITY) ? mn : 0.0f;
     float part = 0.0f;
