@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="mixed256_llama3_bf16",
                     choices=["mixed256_llama3_bf16", "greedy512_quantized", "nucleus1024_qwen_fp32",
-                             "steps8_smollm_mixed", "engine_step_smollm2"])
+                             "steps8_smollm_mixed", "engine_step_smollm2", "lm_head_smollm2"])
     ap.add_argument("--copies", type=int, default=0, help="logits copies to rotate over (default: > 256 MB)")
     ap.add_argument("--cpu-steps", type=int, default=5, help="CPU baseline steps (median)")
     ap.add_argument("--cpu-rows", type=int, default=0, help="CPU baseline rows per step (0: all)")
@@ -216,6 +216,88 @@ def engine_sampler_kernel_us(cap) -> float:
     return round(e0.elapsed_time(e1) * 1e3 / 50, 3)
 
 
+def lm_head_bench(args):
+    """The fused lm_head + greedy kernel at the smollm2-135m head (bf16 hidden [64, 576],
+    weight [49152, 576]; pagedbatch/model.py:283 then sampling.py:12-13) against the unfused
+    path (torch's bf16 Linear, then pbs_argmax over the logits it wrote). Weights rotate
+    over 5 copies (283 MB) so HBM, not the Infinity Cache, serves them. Kernel times are
+    HIP events around 100 back-to-back launches on the launch stream."""
+    import torch
+    import torch.nn.functional as F
+
+    from pagedbatch_amd import _lib
+    from pagedbatch_amd.lm_head import lm_head_argmax
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    rows, hdim, vocab = 64, 576, 49152
+    g = torch.Generator().manual_seed(0)
+    hidden = torch.randn(rows, hdim, generator=g).to(torch.bfloat16).to(dev)
+    w0 = (torch.randn(vocab, hdim, generator=g) * 0.02).to(torch.bfloat16)
+    copies = 5
+    ws = [w0.to(dev) for _ in range(copies)]
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+
+    def timed(fn, n=100):
+        for i in range(10):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    def unfused(i):
+        logits = F.linear(hidden, ws[i % copies])
+        rc = lib.pbs_argmax(logits.data_ptr(), _lib.DTYPE_BF16, rows, rows, vocab, vocab, None, tok.data_ptr(),
+                            st.data_ptr(), stream.cuda_stream)
+        assert rc == 0
+
+    us_fused = timed(lambda i: lm_head_argmax(hidden, ws[i % copies]))
+    us_fused_nologits = timed(lambda i: lm_head_argmax(hidden, ws[i % copies], want_logits=False))
+    us_linear = timed(lambda i: F.linear(hidden, ws[i % copies]))
+    us_unfused = timed(unfused)
+    # parity of the measured kernels: the fused tokens against the argmax of their own
+    # logits and against the unfused path's tokens where torch's logits agree
+    logits, t_f = lm_head_argmax(hidden, ws[0])
+    unfused(0)
+    torch.cuda.synchronize()
+    same_logits = (logits == F.linear(hidden, ws[0])).float().mean().item()
+    agree = (t_f == tok).float().mean().item()
+    wbytes = vocab * hdim * 2
+    traffic = wbytes + rows * hdim * 2 + rows * vocab * 2
+    flops = 2.0 * rows * hdim * vocab
+    out = {
+        "metric": "lm_head + greedy per decode step (us), bf16 [64, 576] x [49152, 576]",
+        "value": round(us_fused, 3),
+        "unit": "us",
+        "higher_is_better": False,
+        "n_gpus": 1,
+        "dtype": "bf16 (fp32 accumulation)",
+        "data": "synthetic (random hidden and weights, seed 0)",
+        "config": {"workload": "lm_head_smollm2", "rows": rows, "hidden": hdim, "vocab": vocab,
+                   "weight_copies_rotated": copies},
+        "us_fused_with_logits": round(us_fused, 3),
+        "us_fused_greedy_only": round(us_fused_nologits, 3),
+        "us_torch_linear": round(us_linear, 3),
+        "us_torch_linear_then_pbs_argmax": round(us_unfused, 3),
+        "roofline": {"bound": "hbm", "achieved": round(traffic / us_fused / 1e3, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(traffic / us_fused / 1e3 / HBM_PEAK_GBPS, 4),
+                     "algorithmic_bytes_per_launch": traffic,
+                     "mfma_tflops": round(flops / us_fused / 1e6, 1), "mfma_peak_tflops": 2500.0},
+        "roofline_greedy_only": {"achieved": round((wbytes + rows * hdim * 2) / us_fused_nologits / 1e3, 1),
+                                 "unit": "GB/s"},
+        "parity": {"logits_equal_to_torch_linear": round(same_logits, 6), "tokens_equal_to_unfused": round(agree, 4)},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def engine_step(args):
     """The end-to-end engine step (smollm2-135m-random, 64 requests x 128 prompt + 128
     output tokens, half greedy, half top-k=50 / top-p=0.9): decode throughput (`value`:
@@ -237,6 +319,9 @@ def engine_step(args):
     print("[bench] engine step: batched sampling, paged-attention decode kernel", file=sys.stderr, flush=True)
     tf, out_f = es.run(shape, **kw, fused_decode=True, capture_steps=(kw["output_len"] - 1,))
     sampler_kernel_us = engine_sampler_kernel_us(tf.captures[0])
+    print("[bench] engine step: fused lm_head + greedy, paged-attention decode kernel", file=sys.stderr, flush=True)
+    th, out_h = es.run(shape, **kw, fused_decode=True, fused_head=True)
+    agree_head = sum(a == b for x, y in zip(out_f, out_h) for a, b in zip(x, y)) / sum(len(x) for x in out_f)
     # the fused attention rounds differently in the last fp32 bits, which the bf16 o_proj
     # input can turn into different tokens later in a sequence: report the agreement
     agree = sum(a == b for x, y in zip(out_b, out_f) for a, b in zip(x, y)) / sum(len(x) for x in out_b)
@@ -249,7 +334,7 @@ def engine_step(args):
                 "sample_share": round(sum(smp) / (sum(fwd) + sum(smp)), 4),
                 "prefill_forward_ms": round(1e3 * t.forward_s[0], 3), "prefill_sample_ms": round(1e3 * t.sample_s[0], 4)}
 
-    b, r, f = split(tb), split(tr), split(tf)
+    b, r, f, hd = split(tb), split(tr), split(tf), split(th)
     step_ms = f["forward_ms"] + f["sample_ms"]
     # the batched call runs the stop check (engine.py:173-182) on the device after the
     # sampler and brings the reasons back with the tokens: every request ends on "length"
@@ -264,6 +349,10 @@ def engine_step(args):
                    "block_size": 16, "mix": "half greedy, half top_k=50 top_p=0.9 T=1.0",
                    "decode_attention": "paged-attention kernel (pba_decode_attention)"},
         "fused_decode_attention": f, "batched_sampling": b, "per_row_sampling": r,
+        "fused_lm_head": {**hd, "note": "forward ends at the final hidden state; sample_ms includes the lm_head "
+                                        "GEMM (pbs_lm_head_argmax) and the stochastic rows' sampling",
+                          "ms_per_step": round(hd["forward_ms"] + hd["sample_ms"], 4),
+                          "token_agreement_vs_torch_head": round(agree_head, 4)},
         "same_tokens_batched_vs_per_row": same, "token_agreement_fused_vs_torch_attention": round(agree, 4),
         "stop_check": "on the device after the sampler, reasons in the tokens' copy back (in sample_ms)",
         "sampler_kernel_us": sampler_kernel_us,
@@ -281,6 +370,9 @@ def main():
 
     if args.workload == "engine_step_smollm2":
         engine_step(args)
+        return
+    if args.workload == "lm_head_smollm2":
+        lm_head_bench(args)
         return
 
     import numpy as np

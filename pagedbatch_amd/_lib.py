@@ -38,6 +38,9 @@ FINISH_NONE, FINISH_STOP, FINISH_LENGTH = 0, 1, 2
 # the C symbols include/pbattn.h declares
 ATTN_SYMBOLS = ("pba_decode_attention",)
 
+# the C symbols include/pblmhead.h declares
+LMHEAD_SYMBOLS = ("pbs_lm_head_workspace_bytes", "pbs_lm_head_argmax")
+
 # the C symbols include/pbsample.h declares, in declaration order
 SYMBOLS = ("pbs_abi_version", "pbs_last_error", "pbs_workspace_bytes", "pbs_sample", "pbs_sample_debug",
            "pbs_argmax", "pbs_finish_reasons")
@@ -164,6 +167,22 @@ def load(path: str | None = None):
             _c.c_int,  # max_context
             _c.c_float,  # scale
             _c.c_void_p,  # out
+            _c.c_void_p,  # stream
+        ]
+        lib.pbs_lm_head_workspace_bytes.restype = _c.c_size_t
+        lib.pbs_lm_head_workspace_bytes.argtypes = [_c.c_int64, _c.c_int64]
+        lib.pbs_lm_head_argmax.restype = _c.c_int
+        lib.pbs_lm_head_argmax.argtypes = [
+            _c.c_void_p,  # hidden
+            _c.c_int64,  # hidden_stride
+            _c.c_void_p,  # weight
+            _c.c_int64,  # rows
+            _c.c_int64,  # hidden_dim
+            _c.c_int64,  # vocab
+            _c.c_void_p,  # out_logits
+            _c.c_void_p,  # out_token
+            _c.c_void_p,  # workspace
+            _c.c_size_t,  # workspace_bytes
             _c.c_void_p,  # stream
         ]
         v = lib.pbs_abi_version()

@@ -1,8 +1,9 @@
 """Build libpbsample.so in-tree with hipcc for gfx950.
 
-``python -m pagedbatch_amd.build`` compiles ``csrc/pbsample.hip`` (the sampler) and
-``csrc/pbattn.hip`` (the paged-attention decode kernel) into
-``pagedbatch_amd/libpbsample.so`` (the file ``_lib.py`` loads). The sampler is compiled
+``python -m pagedbatch_amd.build`` compiles ``csrc/pbsample.hip`` (the sampler),
+``csrc/pbattn.hip`` (the paged-attention decode kernel) and ``csrc/pblmhead.hip`` (the
+fused lm_head + greedy kernel) into ``pagedbatch_amd/libpbsample.so`` (the file
+``_lib.py`` loads). The sampler is compiled
 as several translation units in parallel (one per logits type, ``-DPBS_TU_DTYPE=n``, and
 one for the C ABI, ``-DPBS_TU_ABI``), then everything is linked into one shared library.
 Packed-FP32 instruction selection is disabled (``-packed-fp32-ops``); the kernels are
@@ -21,7 +22,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "pbsample.hip")
 ATTN = os.path.join(HERE, "csrc", "pbattn.hip")
-SRCS = [SRC, ATTN]
+LMHEAD = os.path.join(HERE, "csrc", "pblmhead.hip")
+SRCS = [SRC, ATTN, LMHEAD]
 OUT = os.path.join(HERE, "libpbsample.so")
 ARCH = os.environ.get("PBS_OFFLOAD_ARCH", "gfx950")
 
@@ -32,6 +34,7 @@ UNITS = [
     (SRC, ["-DPBS_TU_DTYPE=0"], "pbsample_f32.o"),
     (SRC, ["-DPBS_TU_ABI"], "pbsample_abi.o"),
     (ATTN, [], "pbattn.o"),
+    (LMHEAD, [], "pblmhead.o"),
 ]
 
 

@@ -101,10 +101,11 @@ class Model:
 
     @torch.no_grad()
     def forward(self, tokens: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor, seq_slots: torch.Tensor,
-                q_len: int, cache: "PagedKV", fused_decode: bool = False) -> torch.Tensor:
+                q_len: int, cache: "PagedKV", fused_decode: bool = False, hidden_only: bool = False) -> torch.Tensor:
         """``tokens``/``pos``/``slots``: [B * q_len] (sequence-major); ``seq_slots``: [B, L] the
         cache slots of each sequence's whole context, new tokens last. Returns [B, vocab]
-        logits of each sequence's last token. ``fused_decode`` runs decode steps
+        logits of each sequence's last token (with ``hidden_only``, its final hidden state
+        [B, hidden] instead, for the fused lm_head). ``fused_decode`` runs decode steps
         (``q_len == 1``) through the paged-attention kernel (``attention.decode_attention``)
         instead of the gather + matmul + softmax below."""
         s = self.shape
@@ -144,7 +145,7 @@ class Model:
             gu = h @ p["gate_up"]
             x = x + (F.silu(gu[:, : s.intermediate_size]) * gu[:, s.intermediate_size :]) @ p["down"]
         last = self._rms(x.view(B, q_len, -1)[:, -1], self.norm)
-        return last @ self.head
+        return last.contiguous() if hidden_only else last @ self.head
 
 
 class PagedKV:
@@ -201,7 +202,7 @@ class StepTimes:
 
 def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len: int = 128, block_size: int = 16,
         device: str | torch.device = "cuda", seed: int = 0, per_row: bool = False,
-        fused_decode: bool = False, capture_steps=()) -> tuple[StepTimes, list[list[int]]]:
+        fused_decode: bool = False, capture_steps=(), fused_head: bool = False) -> tuple[StepTimes, list[list[int]]]:
     """Prefill every prompt, then decode in lockstep until each request has ``output_len``
     tokens. Half the requests are greedy, half top-k=50 / top-p=0.9 at temperature 1.0; the
     unseeded ones share one engine generator (engine.py:58). The batched path samples with
@@ -209,8 +210,12 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
     check of engine.py:173-182 in the same launch sequence and copy back; the model has no
     EOS here, so every request runs to its length limit); ``per_row`` samples with one
     ``sample_token`` call per sequence (the reference loop, unhoisted). ``fused_decode``
-    runs the decode steps' attention through the paged-attention kernel. Returns the time
-    split and the generated tokens."""
+    runs the decode steps' attention through the paged-attention kernel. ``fused_head``
+    computes the logits with the fused lm_head + greedy kernel (``lm_head.lm_head_argmax``,
+    model.py:283): greedy rows take its tokens, the stochastic rows are sampled from the
+    logits it writes (``rows=``), and a step with no stochastic row writes no logits. The
+    forward time then ends at the final hidden state and the sampling time includes the
+    head. Returns the time split and the generated tokens."""
     device = torch.device(device)
     model = Model(shape, device, seed=seed)
     cache = PagedKV(shape, num_seqs, prompt_len + output_len, block_size, device, torch.bfloat16)
@@ -233,9 +238,18 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
         seq_slots = cache.slots(seq.view(-1, 1), ctx)
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
-        logits = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache, fused_decode)
+        out_f = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache, fused_decode,
+                              hidden_only=fused_head)
         torch.cuda.synchronize(device)
         t1 = time.perf_counter()
+        if fused_head:
+            toks, reasons = fused_head_step(model, out_f, params, gens, temps, n_out=len(out[0]) + 1)
+            times.reasons.append(reasons)
+            t2 = time.perf_counter()
+            times.forward_s.append(t1 - t0)
+            times.sample_s.append(t2 - t1)
+            return toks
+        logits = out_f
         cap = None
         if idx in capture_steps:
             # the uniforms this step's rows will draw: from a copy of the engine generator
@@ -261,6 +275,29 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
             cap.tokens = list(toks)
             times.captures.append(cap)
         return toks
+
+    def fused_head_step(model, hidden, params, gens, temps, n_out):
+        from .finish import finish_reasons
+        from .lm_head import lm_head_argmax
+
+        stoch = [i for i in range(num_seqs) if temps[i] != 0]
+        greedy = [i for i in range(num_seqs) if temps[i] == 0]
+        logits, gtok = lm_head_argmax(hidden, model.embed, want_logits=bool(stoch))
+        rule = FinishRule(ignore_eos=False, stop_token_ids=(), num_output=n_out, max_tokens=output_len,
+                          num_tokens=prompt_len + n_out)
+        toks: list = [0] * num_seqs
+        reasons: list = [None] * num_seqs
+        if stoch:
+            st, sr = sample_and_finish(logits, [params[i] for i in stoch], [gens[i] for i in stoch],
+                                       [rule] * len(stoch), None, prompt_len + output_len, rows=stoch)
+            for j, i in enumerate(stoch):
+                toks[i], reasons[i] = st[j], sr[j]
+        if greedy:
+            gsel = gtok[torch.tensor(greedy, device=gtok.device)]
+            gr = finish_reasons(gsel, [rule] * len(greedy), None, prompt_len + output_len)
+            for j, (i, t) in enumerate(zip(greedy, gsel.cpu().tolist())):
+                toks[i], reasons[i] = t, gr[j]
+        return toks, reasons
 
     toks = step(0, prompts.to(device), 0, prompt_len)
     for i, t in enumerate(toks):

@@ -19,6 +19,7 @@ from pagedbatch_amd import sampling as smp
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "pbsample.h")
 ATTN_HEADER = os.path.join(ROOT, "include", "pbattn.h")
+LMHEAD_HEADER = os.path.join(ROOT, "include", "pblmhead.h")
 
 
 # ---------------------------------------------------------------- SamplingParams mirror
@@ -165,8 +166,10 @@ def test_library_exports_every_header_symbol():
     assert set(names) == set(_lib.SYMBOLS), (names, _lib.SYMBOLS)
     attn = _header_functions(ATTN_HEADER)
     assert set(attn) == set(_lib.ATTN_SYMBOLS), (attn, _lib.ATTN_SYMBOLS)
+    lmh = _header_functions(LMHEAD_HEADER)
+    assert set(lmh) == set(_lib.LMHEAD_SYMBOLS), (lmh, _lib.LMHEAD_SYMBOLS)
     raw = ctypes.CDLL(_lib.LIB_PATH)
-    for n in names + attn:
+    for n in names + attn + lmh:
         assert hasattr(raw, n), n
     assert lib.pbs_abi_version() == _lib.ABI_VERSION
     m = re.search(r"#define PBS_ABI_VERSION (\d+)", open(HEADER).read())
@@ -226,6 +229,26 @@ def test_abi_rejects_bad_arguments_before_any_device_work(kw, code, msg):
     lib = _lib.load()
     assert _call(lib, **kw) == code
     assert msg in _lib.last_error(lib)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    ({"hdim": 100}, _lib.ERR_INVALID_ARGUMENT, "multiple of 64"),
+    ({"stride": 60}, _lib.ERR_INVALID_ARGUMENT, "hidden_stride"),
+    ({"vocab": 0}, _lib.ERR_INVALID_ARGUMENT, "vocab"),
+    ({"weight": None}, _lib.ERR_INVALID_ARGUMENT, "null"),
+    ({"vocab": 1 << 24, "hdim": 128, "stride": 128}, _lib.ERR_INVALID_ARGUMENT, "2^31"),
+    ({"hidden": (1 << 20) + 8}, _lib.ERR_INVALID_ARGUMENT, "16-byte"),
+    ({"ws_bytes": 8}, _lib.ERR_WORKSPACE, "workspace"),
+])
+def test_lm_head_abi_rejects_bad_arguments(kw, code, msg):
+    lib = _lib.load()
+    a = dict(hidden=1 << 20, stride=64, weight=1 << 20, rows=4, hdim=64, vocab=1000, ws_bytes=1 << 20)
+    a.update(kw)
+    rc = lib.pbs_lm_head_argmax(a["hidden"], a["stride"], a["weight"], a["rows"], a["hdim"], a["vocab"], None,
+                                1 << 20, 1 << 20, a["ws_bytes"], None)
+    assert rc == code
+    assert msg in _lib.last_error(lib)
+    assert lib.pbs_lm_head_workspace_bytes(4, 1000) == 4 * 16 * 8
 
 
 def test_abi_zero_rows_is_a_no_op():
