@@ -47,6 +47,20 @@ int pbs_lm_head_argmax(const uint16_t* hidden, int64_t hidden_stride, const uint
                        int64_t hidden_dim, int64_t vocab, uint16_t* out_logits, int32_t* out_token,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * pbs_lm_head_argmax without a workspace argument and without any allocation, for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). It has no counterpart in the reference. The kernels use the library's
+ * own per-GPU scratch array (4 MiB, kept until the process ends), so rows * ceil(vocab /
+ * 64) must not exceed 524288 (PBS_ERR_WORKSPACE otherwise; e.g. 256 rows of a 131072
+ * vocab). The scratch belongs to the device current at the call; its address is looked up
+ * on the first call on each device. Calls that overlap on one GPU (several streams or
+ * threads at once) share that array and race: serialize them.
+ */
+int pbs_lm_head_argmax_noalloc(const uint16_t* hidden, int64_t hidden_stride, const uint16_t* weight, int64_t rows,
+                               int64_t hidden_dim, int64_t vocab, uint16_t* out_logits, int32_t* out_token,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,7 +39,7 @@ FINISH_NONE, FINISH_STOP, FINISH_LENGTH = 0, 1, 2
 ATTN_SYMBOLS = ("pba_decode_attention",)
 
 # the C symbols include/pblmhead.h declares
-LMHEAD_SYMBOLS = ("pbs_lm_head_workspace_bytes", "pbs_lm_head_argmax")
+LMHEAD_SYMBOLS = ("pbs_lm_head_workspace_bytes", "pbs_lm_head_argmax", "pbs_lm_head_argmax_noalloc")
 
 # the C symbols include/pbsample.h declares, in declaration order
 SYMBOLS = ("pbs_abi_version", "pbs_last_error", "pbs_workspace_bytes", "pbs_sample", "pbs_sample_debug",
@@ -185,6 +185,8 @@ def load(path: str | None = None):
             _c.c_size_t,  # workspace_bytes
             _c.c_void_p,  # stream
         ]
+        lib.pbs_lm_head_argmax_noalloc.restype = _c.c_int
+        lib.pbs_lm_head_argmax_noalloc.argtypes = lib.pbs_lm_head_argmax.argtypes[:8] + [_c.c_void_p]
         v = lib.pbs_abi_version()
         if v != ABI_VERSION:
             raise SamplerUnavailable(f"{p} has ABI version {v}, this package expects {ABI_VERSION}")

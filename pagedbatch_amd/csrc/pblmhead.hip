@@ -29,6 +29,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "pblmhead.h"
 #include "pbsample.h"
 
@@ -424,6 +426,36 @@ __global__ __launch_bounds__(256) void k_lmhead_finish(const unsigned long long*
 
 }  // namespace pbl
 
+// The workspace of pbs_lm_head_argmax_noalloc: one array per GPU, in the library's own
+// device memory, kept until the process ends. Host code never passes `scratch` itself (its
+// host-side name is not a device address): the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t SCRATCH_KEYS = (size_t)1 << 19;  // 4 MiB: rows x 64-column tiles of 8 bytes
+static __device__ __align__(256) unsigned long long scratch[SCRATCH_KEYS];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[MAX_DEVICES];  // scratch's device address on each GPU (null until its first call)
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= MAX_DEVICES) return pbs::report_errorf(PBS_ERR_HIP, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return pbs::report_errorf(PBS_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return PBS_OK;
+}
+}  // namespace
+
 extern "C" {
 
 size_t pbs_lm_head_workspace_bytes(int64_t rows, int64_t vocab) {
@@ -485,6 +517,24 @@ int pbs_lm_head_argmax(const uint16_t* hidden, int64_t hidden_stride, const uint
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return PBS_OK;
+}
+
+int pbs_lm_head_argmax_noalloc(const uint16_t* hidden, int64_t hidden_stride, const uint16_t* weight, int64_t rows,
+                               int64_t hidden_dim, int64_t vocab, uint16_t* out_logits, int32_t* out_token,
+                               void* stream) {
+  if (rows < 0) return pbs::report_errorf(PBS_ERR_INVALID_ARGUMENT, "rows is negative (%lld)", (long long)rows);
+  if (rows == 0) return PBS_OK;
+  if (vocab > 0 && pbs_lm_head_workspace_bytes(rows, vocab) > sizeof(scratch))
+    return pbs::report_errorf(PBS_ERR_WORKSPACE,
+                              "rows x vocab tiles need %zu bytes of scratch, the library holds %zu per GPU "
+                              "(rows * ceil(vocab / 64) <= %zu)",
+                              pbs_lm_head_workspace_bytes(rows, vocab), sizeof(scratch), SCRATCH_KEYS);
+  // every other argument is checked by pbs_lm_head_argmax, before anything is launched
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != PBS_OK) return rc;
+  return pbs_lm_head_argmax(hidden, hidden_stride, weight, rows, hidden_dim, vocab, out_logits, out_token, ws,
+                            sizeof(scratch), stream);
 }
 
 }  // extern "C"
