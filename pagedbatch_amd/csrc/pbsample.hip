@@ -307,6 +307,25 @@ __device__ __forceinline__ float raw_to_float(uint32_t raw) {
   }
 }
 
+// the largest element of one 16-byte vector (NaN ignored); nan |= the vector holds a NaN
+template <int DT>
+__device__ __forceinline__ float vec_max(const u4& q, bool& nan) {
+  constexpr int EPV = DTraits<DT>::EPV;
+  float e[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) e[i] = raw_to_float<DT>(elem_raw<DT>(q, i));
+  bool n = false;
+#pragma unroll
+  for (int i = 0; i < EPV; i += 2) n |= __builtin_isunordered(e[i], e[i + 1]);
+  nan |= n;
+#pragma unroll
+  for (int w = 1; w < EPV; w *= 2) {
+#pragma unroll
+    for (int i = 0; i + w < EPV; i += 2 * w) e[i] = fmaxf(e[i], e[i + w]);
+  }
+  return e[0];
+}
+
 // Order-preserving keys. -0 is folded onto +0 first so that the two zeros, which compare
 // equal, form one tie group. NaNs land above +inf (positive) or below -inf (negative);
 // stochastic rows holding NaN are rejected before any key is used.
@@ -2841,21 +2860,57 @@ __device__ __forceinline__ void sample_row(const KArgs& a, Smem& s, Src& src, in
     float bv = -INFINITY;
     int bi = INT32_MAX;
     int nan_i = INT32_MAX;
-    src.stream([&](int, const u4& q, int base, bool vvalid) {
+    if constexpr (Src::kVector) {
+      // per vector: its maximum, one compare with the running best and a copy of the best
+      // vector, whose first element equal to the maximum is resolved at the end; a NaN is
+      // only flagged, and a row holding one is scanned again for its first NaN
+      bool nan = false;
+      int bvec = -1;
+      u4 bq = {0u, 0u, 0u, 0u};
+      src.stream([&](int, const u4& q, int base, bool vvalid) {
+        if (vvalid) {
+          // vectors reach a thread in increasing index order: strict > keeps the first
+          const float m = vec_max<DT>(q, nan);
+          const bool up = m > bv;
+          bv = up ? m : bv;
+          bvec = up ? base : bvec;
+          bq = up ? q : bq;
+        }
+      });
+      if (bvec >= 0) {
+        int e = EPV - 1;
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        const float v = raw_to_float<DT>(elem_raw<DT>(q, e));
-        const int idx = base + e;
-        if (elem_valid(src, vvalid, idx)) {
-          // elements arrive in increasing index order per thread: strict > keeps the first
-          if (v > bv || (bi == INT32_MAX && v == v)) {
-            bv = v;
-            bi = idx;
+        for (int i = EPV - 2; i >= 0; --i) e = (raw_to_float<DT>(elem_raw<DT>(bq, i)) == bv) ? i : e;
+        bi = bvec + e;
+      }
+      if (__syncthreads_or(nan)) {
+        // re-read from memory (the row's registers are dead by now): each thread's first NaN
+        const uint8_t* rp = (const uint8_t*)a.logits + (size_t)lrow * (size_t)a.row_stride * elt;
+        for (int i = (int)threadIdx.x; i < a.vocab; i += NT) {
+          const float v = B16 ? raw_to_float<DT>(((const uint16_t*)rp)[i]) : raw_to_float<DT>(((const uint32_t*)rp)[i]);
+          if (v != v) {
+            nan_i = i;
+            break;
           }
-          nan_i = (v != v) ? min(nan_i, idx) : nan_i;
         }
       }
-    });
+    } else {
+      src.stream([&](int, const u4& q, int base, bool vvalid) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          const float v = raw_to_float<DT>(elem_raw<DT>(q, e));
+          const int idx = base + e;
+          if (elem_valid(src, vvalid, idx)) {
+            // elements arrive in increasing index order per thread: strict > keeps the first
+            if (v > bv || (bi == INT32_MAX && v == v)) {
+              bv = v;
+              bi = idx;
+            }
+            nan_i = (v != v) ? min(nan_i, idx) : nan_i;
+          }
+        }
+      });
+    }
     nan_i = block_min_i(nan_i, s);
     block_argmax(bv, bi, s);
     if (threadIdx.x == 0) {
@@ -3020,23 +3075,6 @@ int launch_dt(const KArgs& a, int64_t rows, bool vec, hipStream_t stream) {
 constexpr int NT_AM = 256;
 constexpr int G_AM = 4;
 
-template <int DT>
-__device__ __forceinline__ float vec_max(const u4& q, bool& nan) {
-  constexpr int EPV = DTraits<DT>::EPV;
-  float e[EPV];
-#pragma unroll
-  for (int i = 0; i < EPV; ++i) e[i] = raw_to_float<DT>(elem_raw<DT>(q, i));
-  bool n = false;
-#pragma unroll
-  for (int i = 0; i < EPV; i += 2) n |= __builtin_isunordered(e[i], e[i + 1]);
-  nan |= n;
-#pragma unroll
-  for (int w = 1; w < EPV; w *= 2) {
-#pragma unroll
-    for (int i = 0; i + w < EPV; i += 2 * w) e[i] = fmaxf(e[i], e[i + w]);
-  }
-  return e[0];
-}
 
 template <int DT, bool VEC>
 __global__ __launch_bounds__(NT_AM) void k_argmax(KArgs a) {
