@@ -1,10 +1,11 @@
 // pbsample.hip -- gfx950 (MI355X) token sampler: greedy / temperature / top-k / top-p / draw.
 //
 // Replaces the per-row torch op chain of pagedbatch/sampling.py:10-27 (called once per
-// row from pagedbatch/engine.py:133-139) with one launch per engine step: one 1024-thread
-// workgroup per output row, the row held in VGPRs after a single coalesced 16-byte-load
-// pass over HBM (or re-streamed from memory when it does not fit), per-row selection
-// state in LDS.
+// row from pagedbatch/engine.py:133-139) with one launch per engine step: one 512-thread
+// workgroup (8 waves) per output row, the row held in VGPRs after a single coalesced
+// 16-byte-load pass over HBM (or re-streamed from memory when it does not fit), per-row
+// selection state in LDS. Steps whose rows are all greedy take pbs_argmax's kernel
+// (k_argmax) instead: no histogram, so several small workgroups share a CU.
 //
 // Selection works on order-preserving integer keys ("ords") of the values:
 //   16-bit logits (bf16 / fp16): every distinct value has its own ord, so a 64K-bin
@@ -13,8 +14,11 @@
 //     count * weight, computed once per distinct value in fp64. Top-k threshold, top-p
 //     cutoff and the inverse-CDF draw are prefix searches over that histogram in
 //     descending value order; only "which of the tied tokens" looks at indices again.
-//   fp32 logits: x = fp32(v)/T per element (exact division), searches by bisection on
-//     32-bit ords of x with exact fp64 mass sums.
+//   fp32 logits: a histogram of the top 16 bits of each x = fp32(v)/T (exact division)
+//     bounds every cumulative mass; one more pass gathers the elements of the few bins
+//     the searches land in and sums the exact mass above them; the searches finish in
+//     that list. Rows the list cannot hold fall back to bisection on 32-bit ords with
+//     exact fp64 mass sums.
 //
 // The order everywhere is (scaled value descending, index ascending): the order
 // pagedbatch's top-p sort establishes (sampling.py:19), with ties broken by index.
@@ -520,7 +524,7 @@ struct __align__(16) Smem {
 };
 
 // ---------------------------------------------------------------------------------------
-// block reductions (1024 threads, 16 waves)
+// block reductions (NT = 512 threads, NWAVE = 8 waves)
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ float block_max_f(float v, Smem& s) {
   v = wmax_f32(v);
