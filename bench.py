@@ -479,8 +479,10 @@ def main():
         raw = raw.view(torch.int16).numpy().view(np.uint16) if raw.dtype == torch.bfloat16 else raw.numpy()
         dt = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}[w.logits.dtype]
         refs = oracle.sample_batch(raw, dt, w.temperature[:n], w.top_k[:n], w.top_p[:n], w.uniform[:n])
-        rep = compare_rows(tokens[:n], status[:n], refs, [t == 0 for t in w.temperature[:n]])
-        parity = {"rows": n, "ok": rep.ok(), "tokens_checked": rep.checked_tokens, "exempt": rep.exempt_tokens}
+        rep = compare_rows(tokens[:n], status[:n], refs, [t == 0 for t in w.temperature[:n]], top_p=w.top_p[:n],
+                           uniform=w.uniform[:n])
+        parity = {"rows": n, "ok": rep.ok(), "tokens_checked": rep.checked_tokens,
+                  "tokens_in_band_checked_to_band_bar": rep.exempt_tokens}
 
     traffic, traffic_note = committed_traffic(args.workload)
     surface = python_surface(w, bufs, copies, rows)
