@@ -336,14 +336,16 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) f.acc[i][j] = (f32x16){};
-    // the hidden block: 64 rows (zeros past the last) x hidden_dim, 16 bytes per piece,
-    // eight loads in flight per thread before any is stored
+    // The hidden block (64 rows, zeros past the last, x hidden_dim; 16 bytes per piece):
+    // up to 24 pieces per thread in flight at once, and the first weight chunks go out
+    // right behind them, so the two latencies overlap.
     const int per_row = a.hdim / 8;
     const int npiece = TM * per_row;
-    for (int q0 = tid; q0 < npiece; q0 += 8 * 64 * LW_WAVES) {
-      u4 v[8];
+    constexpr int SB = 24;
+    for (int q0 = tid; q0 < npiece; q0 += SB * 64 * LW_WAVES) {
+      u4 v[SB];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < SB; ++u) {
         const int q = q0 + u * 64 * LW_WAVES;
         const int r = q / per_row, c = q - r * per_row;
         v[u] = q < npiece ? __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -351,21 +353,21 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
                                                    0, 0))
                           : (u4){0u, 0u, 0u, 0u};
       }
+      // (every thread takes this first batch: npiece >= 64 * 8 > 64 * LW_WAVES)
+      if (q0 == tid && active) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+        for (int d = 0; d < WD; ++d)
+          if (d < nk) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
         const int q = q0 + u * 64 * LW_WAVES;
         const int r = q / per_row, c = q - r * per_row;
         if (q < npiece) *(u4*)(hb + r * hs + 8 * c) = v[u];
       }
-    }
-    // the first weight chunks go out while the block settles
-    if (active) {
-#pragma unroll
-      for (int d = 0; d < WD; ++d)
-        if (d < nk) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
-        }
     }
     __syncthreads();
     if (active) {
