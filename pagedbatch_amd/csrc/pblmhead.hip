@@ -19,16 +19,20 @@
 // hidden x 2 bytes, 56.6 MB for a 49152 x 576 head) is read from HBM once per row block:
 // at decode batch sizes the kernel is HBM-bound on it, not MFMA-bound.
 //
-// Epilogue: the 64 x 64 fp32 tile is rounded to bf16 (nearest, ties to even) into LDS;
-// from there the wave writes the logits rows (when asked) and each lane scans one row of
-// the tile for its largest value as a key (ordered bf16 value, then the complement of the
-// column, so the maximum key is the first maximum; NaN above everything), one 64-bit key
-// per (row, tile) into the workspace. A second, tiny kernel reduces each row's keys to
-// its token.
+// Epilogue: the 64 x 64 fp32 tile goes to LDS; from there the wave writes the logits rows
+// in bf16 (when asked; nearest, ties to even) and each lane takes one row of the tile: its
+// largest fp32 value (NaN-propagating), rounded to bf16 once, fixes the lowest fp32 value
+// that rounds to the same logit, and the first column at or above that bound is the row's
+// first maximum among the bf16 logits. One 64-bit key per (row, tile) goes to the
+// workspace (ordered bf16 value, then the complement of the column, so the largest key is
+// the first maximum; NaN above everything). A second, tiny kernel reduces each row's keys
+// to its token.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "pblmhead.h"
@@ -48,7 +52,7 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 constexpr int TM = 64;        // rows per block: two 32-row MFMA tiles
 constexpr int TN = 64;        // vocab columns per workgroup: two 32-column MFMA tiles
 constexpr int KC = 64;        // hidden elements per chunk: four MFMA steps of 16
-constexpr int LROW = TN + 2;  // bf16 per tile row in LDS (the padding spreads the banks)
+constexpr int TST = TN + 8;   // fp32 per tile row in LDS (rows 4 apart sit 32 banks apart)
 constexpr int WD = 4;         // weight chunks in flight per wave
 
 struct Args {
@@ -73,9 +77,6 @@ __device__ __forceinline__ uint32_t ord_bf16(uint32_t r) {
   if ((r & 0x7fffu) > 0x7f80u) return 0xffffu;
   return r ^ ((r & 0x8000u) ? 0xffffu : 0x8000u);
 }
-
-// 32-bit key of a bf16 value in column c (< 64) of a tile: ordered value, then 63 - c
-__device__ __forceinline__ uint32_t tile_key(uint32_t raw, int c) { return (ord_bf16(raw) << 16) | (uint32_t)(63 - c); }
 
 // the lane's 64 bytes of one operand row: four 16-byte buffer loads, the whole offset in
 // the VGPR operand, so rows past the buffer's end read zeros
@@ -133,73 +134,113 @@ __device__ __forceinline__ void ktail(Frags& f, __amdgpu_buffer_rsrc_t wrs, __am
   }
 }
 
-// The 64 x 64 block of one wave: bf16 to the wave's LDS tile, the logits rows from there
-// (when asked), and each tile row's largest key into part[row][tile_id].
-__device__ __forceinline__ void epilogue(const Args& a, uint16_t* tile, const f32x16 (&acc)[2][2], int m0, int n0,
+// The smallest fp32 value whose bf16 rounding (nearest, ties to even) is the bf16 value b;
+// for b = +-0 the smallest one rounding to -0, since -0 and +0 compare equal as logits. b
+// is not NaN. A value x no larger than the row's maximum, whose rounding is b, rounds to b
+// exactly when x >= this bound (the rounding is monotonic).
+__device__ __forceinline__ float bf16_class_low(uint32_t b) {
+  if (b == 0u) b = 0x8000u;
+  const uint32_t odd = b & 1u;  // a tie goes to the even neighbour
+  if (b & 0x8000u) return b == 0xff80u ? -__builtin_inff() : __uint_as_float((b << 16) + 0x8000u - odd);
+  return __uint_as_float((b << 16) - 0x8000u + odd);
+}
+
+// two fp32 values to packed bf16 (v_cvt_pk_bf16_f32: nearest, ties to even; the first in
+// the low half)
+__device__ __forceinline__ uint32_t pack_bf16(float x, float y) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
+}
+
+// The 64 x 64 block of one wave: the fp32 tile to the wave's LDS tile, the bf16 logits rows
+// from there (when asked), and each tile row's first maximum as a key into
+// part[row][tile_id]: the row's largest fp32 value, rounded to bf16 once, gives the bound
+// every value equal to the maximum as a bf16 logit reaches, and the first column at or
+// above it is the first maximum; a NaN anywhere in the row makes the first NaN the answer.
+__device__ __forceinline__ void epilogue(const Args& a, float* tile, const f32x16 (&acc)[2][2], int m0, int n0,
                                          int tile_id, int ntiles, int l, int half, int r32) {
-    // the tile in bf16 to LDS: accumulator register v of lane l holds row
-    // 8 (v / 4) + 4 (l / 32) + v % 4 and column l % 32 of its 32 x 32 tile
+  // accumulator register v of lane l holds row 8 (v / 4) + 4 (l / 32) + v % 4 and column
+  // l % 32 of its 32 x 32 tile
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
-          tile[row * LROW + 32 * j + r32] = (uint16_t)bf16_rne(acc[i][j][v]);
-        }
-    __threadfence_block();  // the wave's tile writes are done before any lane reads them
-    __builtin_amdgcn_wave_barrier();
+      for (int v = 0; v < 16; ++v) {
+        const int row = 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
+        tile[row * TST + 32 * j + r32] = acc[i][j][v];
+      }
+  __threadfence_block();  // the wave's tile writes are done before any lane reads them
+  __builtin_amdgcn_wave_barrier();
 
-    if (a.out_logits) {
-      // eight lanes per row, 16 bytes each; rows and columns past the ends are skipped
+  if (a.out_logits) {
+    // eight lanes per row, eight columns (16 bytes of bf16) each; rows and columns past
+    // the ends are skipped
 #pragma unroll 1
-      for (int r0 = 0; r0 < TM; r0 += 8) {
-        const int row = r0 + (l >> 3);
-        const int c = 8 * (l & 7);
-        const int gr = m0 + row, gc = n0 + c;
-        if (gr < a.rows && gc < a.vocab) {
-          uint16_t* dst = a.out_logits + (int64_t)gr * a.vocab + gc;
-          const uint16_t* src = tile + row * LROW + c;
-          if (gc + 8 <= a.vocab && ((uintptr_t)dst & 15u) == 0u) {
-            const uint32_t* s32 = (const uint32_t*)src;  // c is even and rows are 132 bytes apart
-            u4 q;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = s32[e];
-            *(u4*)dst = q;
-          } else {
-            for (int e = 0; e < 8 && gc + e < a.vocab; ++e) dst[e] = src[e];
-          }
+    for (int r0 = 0; r0 < TM; r0 += 8) {
+      const int row = r0 + (l >> 3);
+      const int c = 8 * (l & 7);
+      const int gr = m0 + row, gc = n0 + c;
+      if (gr < a.rows && gc < a.vocab) {
+        const float4 x0 = *(const float4*)(tile + row * TST + c);
+        const float4 x1 = *(const float4*)(tile + row * TST + c + 4);
+        const u4 q = {pack_bf16(x0.x, x0.y), pack_bf16(x0.z, x0.w), pack_bf16(x1.x, x1.y), pack_bf16(x1.z, x1.w)};
+        uint16_t* dst = a.out_logits + (int64_t)gr * a.vocab + gc;
+        if (gc + 8 <= a.vocab && ((uintptr_t)dst & 15u) == 0u) {
+          *(u4*)dst = q;
+        } else {
+          for (int e = 0; e < 8 && gc + e < a.vocab; ++e) dst[e] = (uint16_t)(q[e >> 1] >> (16 * (e & 1)));
         }
       }
     }
+  }
 
-    // lane l: the largest key of tile row l (two columns per 32-bit LDS read, all reads
-    // in flight); columns past the vocab count as nothing
-    const uint32_t* trow = (const uint32_t*)(tile + l * LROW);
-    const int ncol = min(TN, a.vocab - n0);
-    uint32_t best = 0u;
-    if (ncol == TN) {
+  // lane l: row l of the tile. Columns past the vocab (zero weights, so 0, or NaN beside
+  // an infinite hidden value) are overwritten with -inf first; column 0 always exists, so
+  // the first column at or above any bound is a real one. The logits reads above come
+  // first: the wave's LDS operations complete in order.
+  const int ncol = min(TN, a.vocab - n0);
+  if (ncol < TN) {
+#pragma unroll 1
+    for (int c = ncol; c < TN; ++c) tile[l * TST + c] = -__builtin_inff();
+  }
+  float x[TN];
 #pragma unroll
-      for (int c2 = 0; c2 < TN / 2; ++c2) {
-        const uint32_t q = trow[c2];
-        best = max(best, max(tile_key(q & 0xffffu, 2 * c2), tile_key(q >> 16, 2 * c2 + 1)));
-      }
-    } else {
-      for (int c = 0; c < ncol; ++c) best = max(best, tile_key(tile[l * LROW + c], c));
-    }
-    if (m0 + l < a.rows) {
-      const uint32_t col = (uint32_t)n0 + 63u - (best & 0xffffu);
-      a.part[(int64_t)(m0 + l) * ntiles + tile_id] =
-          ((unsigned long long)(best >> 16) << 32) | (unsigned long long)(0xffffffffu - col);
-    }
+  for (int c4 = 0; c4 < TN / 4; ++c4) {
+    const float4 q = *(const float4*)(tile + l * TST + 4 * c4);
+    x[4 * c4] = q.x, x[4 * c4 + 1] = q.y, x[4 * c4 + 2] = q.z, x[4 * c4 + 3] = q.w;
+  }
+  float m = x[0];  // the largest value; NaN if the row holds one
+#pragma unroll
+  for (int c = 1; c + 1 < TN; c += 2)
+    m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, x[c]), x[c + 1]);
+  m = __builtin_elementwise_maximum(m, x[TN - 1]);
+  uint32_t ord;
+  int first = 0;
+  if (m != m) {  // the first NaN
+    ord = 0xffffu;
+#pragma unroll
+    for (int c = TN - 1; c >= 0; --c) first = (x[c] != x[c]) ? c : first;
+  } else {
+    const uint32_t b = bf16_rne(m);
+    ord = ord_bf16(b);
+    const float lo = bf16_class_low(b);
+#pragma unroll
+    for (int c = TN - 1; c >= 0; --c) first = (x[c] >= lo) ? c : first;
+  }
+  if (m0 + l < a.rows) {
+    const uint32_t col = (uint32_t)(n0 + first);
+    a.part[(int64_t)(m0 + l) * ntiles + tile_id] =
+        ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - col);
+  }
   __threadfence_block();  // the tile is rewritten by the next row block
   __builtin_amdgcn_wave_barrier();
 }
 
 __global__ __launch_bounds__(64) void k_lmhead(Args a) {
-  __shared__ uint16_t tile[TM * LROW];
-    const int l = threadIdx.x;
+  __shared__ float tile[TM * TST];
+  const int l = threadIdx.x;
   const int n0 = blockIdx.x * TN;
   const int half = l >> 5;  // which 32-element half of a chunk the lane reads
   const int r32 = l & 31;   // the lane's row within a 32-row (or 32-column) MFMA tile
@@ -262,6 +303,10 @@ __global__ __launch_bounds__(64) void k_lmhead(Args a) {
 // ---------------------------------------------------------------------------------------
 constexpr int LW_WAVES = 3;
 constexpr int LDS_HMAX = 1024;  // largest hidden_dim of this kernel
+// LDS bytes: the hidden block (64 rows of hidden_dim + 8 bf16), and the waves' fp32 tiles
+// that replace it after the multiplies
+constexpr size_t lds_hidden_bytes(int hdim) { return (size_t)TM * (size_t)(hdim + 8) * 2; }
+constexpr size_t LDS_TILES = (size_t)LW_WAVES * TM * TST * 4;
 
 // weight-only fragments and accumulators of one wave
 struct FragsW {
@@ -284,6 +329,7 @@ __device__ __forceinline__ void kstep_lds(FragsW& f, __amdgpu_buffer_rsrc_t wrs,
   constexpr int B = I % WD;
   u4 h[2][4];
   lds_frags(hb, hs, r32, half, kc, h);
+  __builtin_amdgcn_sched_barrier(0);  // all eight LDS reads go out before the first multiply
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -311,11 +357,13 @@ __device__ __forceinline__ void ktail_lds(FragsW& f, __amdgpu_buffer_rsrc_t wrs,
 }
 
 __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
-  extern __shared__ uint16_t smem[];
+  // the hidden block while the waves multiply, then (after a barrier) the waves' fp32
+  // tiles over it
+  extern __shared__ __align__(16) uint16_t smem[];
   const int hs = a.hdim + 8;  // LDS row stride of the hidden block (the pad spreads the banks)
   uint16_t* hb = smem;        // [TM][hs]
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
-  uint16_t* tile = smem + TM * hs + wv * TM * LROW;
+  float* tile = (float*)smem + wv * TM * TST;
   const int tile_id = blockIdx.x * LW_WAVES + wv;
   const int ntiles = (a.vocab + TN - 1) / TN;
   const int n0 = tile_id * TN;
@@ -336,38 +384,51 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) f.acc[i][j] = (f32x16){};
-    // The hidden block (64 rows, zeros past the last, x hidden_dim; 16 bytes per piece):
-    // up to 24 pieces per thread in flight at once, and the first weight chunks go out
-    // right behind them, so the two latencies overlap.
+    // The hidden block (64 rows, zeros past the last, x hidden_dim; 16 bytes per piece) in
+    // batches of up to 24 pieces per thread in flight. The first weight chunks go out right
+    // behind the last batch, unconditionally (chunks past the row's end or past the
+    // buffer's end read harmless data or zeros, never used), so the wait before that
+    // batch's LDS writes leaves them in flight and the two latencies overlap.
     const int per_row = a.hdim / 8;
     const int npiece = TM * per_row;
-    constexpr int SB = 24;
-    for (int q0 = tid; q0 < npiece; q0 += SB * 64 * LW_WAVES) {
+    constexpr int SB = 24, SSTEP = 64 * LW_WAVES;
+    // piece q -> (row q / per_row, column piece): ((q + 0.5) * fl(1 / per_row)) is within
+    // 2e-3 of (q + 0.5) / per_row for q < 2^14, and that quotient is at least
+    // 0.5 / per_row >= 1 / 256 from an integer, so the truncation is exact
+    const float inv_pr = 1.0f / (float)per_row;
+    const int nbatch = (npiece - tid + SB * SSTEP - 1) / (SB * SSTEP);  // >= 1: npiece >= 512 > tid
+    auto batch_loads = [&](int q0, u4 (&v)[SB]) {
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int q = min(q0 + u * SSTEP, npiece - 1);
+        const int r = (int)(((float)q + 0.5f) * inv_pr), c = q - r * per_row;
+        v[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          hrs, (uint32_t)((((int64_t)(m0 + r)) * a.hstride + 8 * c) * 2), 0, 0));
+      }
+    };
+    // (a clamped piece is the last one, loaded and stored again with the same value)
+    auto batch_stores = [&](int q0, const u4 (&v)[SB]) {
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int q = min(q0 + u * SSTEP, npiece - 1);
+        const int r = (int)(((float)q + 0.5f) * inv_pr), c = q - r * per_row;
+        *(u4*)(hb + r * hs + 8 * c) = v[u];
+      }
+    };
+    for (int b = 0; b + 1 < nbatch; ++b) {
       u4 v[SB];
+      batch_loads(tid + b * SB * SSTEP, v);
+      batch_stores(tid + b * SB * SSTEP, v);
+    }
+    {
+      const int q0 = tid + (nbatch - 1) * SB * SSTEP;
+      u4 v[SB];
+      batch_loads(q0, v);
 #pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const int q = q0 + u * 64 * LW_WAVES;
-        const int r = q / per_row, c = q - r * per_row;
-        v[u] = q < npiece ? __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   hrs, (uint32_t)((((int64_t)(m0 + r)) * a.hstride + 8 * c) * 2),
-                                                   0, 0))
-                          : (u4){0u, 0u, 0u, 0u};
-      }
-      // (every thread takes this first batch: npiece >= 64 * 8 > 64 * LW_WAVES)
-      if (q0 == tid && active) {
+      for (int d = 0; d < WD; ++d)
 #pragma unroll
-        for (int d = 0; d < WD; ++d)
-          if (d < nk) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
-          }
-      }
-#pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const int q = q0 + u * 64 * LW_WAVES;
-        const int r = q / per_row, c = q - r * per_row;
-        if (q < npiece) *(u4*)(hb + r * hs + 8 * c) = v[u];
-      }
+        for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
+      batch_stores(q0, v);
     }
     __syncthreads();
     if (active) {
@@ -387,9 +448,10 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
         case 6: ktail_lds<6>(f, wrs, woff, hb, hs, r32, half, kc0); break;
         default: ktail_lds<7>(f, wrs, woff, hb, hs, r32, half, kc0); break;
       }
-      epilogue(a, tile, f.acc, m0, n0, tile_id, ntiles, l, half, r32);
     }
-    __syncthreads();  // the hidden block and the tiles are rewritten by the next row block
+    __syncthreads();  // every wave's hidden reads are done: the tiles overwrite the block
+    if (active) epilogue(a, tile, f.acc, m0, n0, tile_id, ntiles, l, half, r32);
+    __syncthreads();  // the tiles are read before the next row block's hidden block
   }
 }
 
@@ -439,6 +501,22 @@ namespace {
 constexpr int MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[MAX_DEVICES];  // scratch's device address on each GPU (null until its first call)
+
+// k_lmhead_lds may take more than 64 KiB of dynamic LDS: raise its limit once per device
+std::atomic<bool> g_lds_attr[MAX_DEVICES];
+
+int lds_attribute() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= MAX_DEVICES) return pbs::report_errorf(PBS_ERR_HIP, "device index %d out of range", dev);
+  if (g_lds_attr[dev].load(std::memory_order_acquire)) return PBS_OK;
+  e = hipFuncSetAttribute((const void*)pbl::k_lmhead_lds, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)std::max(pbl::lds_hidden_bytes(pbl::LDS_HMAX), pbl::LDS_TILES));
+  if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+  g_lds_attr[dev].store(true, std::memory_order_release);
+  return PBS_OK;
+}
 
 int scratch_address(void** out) {
   int dev = -1;
@@ -499,15 +577,10 @@ int pbs_lm_head_argmax(const uint16_t* hidden, int64_t hidden_stride, const uint
   a.vocab = (int)vocab;
   const unsigned ntiles = (unsigned)((vocab + pbl::TN - 1) / pbl::TN);
   if (hidden_dim <= pbl::LDS_HMAX) {
-    const size_t lds = ((size_t)pbl::TM * (size_t)(hidden_dim + 8) + (size_t)pbl::LW_WAVES * pbl::TM * pbl::LROW) * 2;
-    static bool attr_set = false;  // every device takes the same attribute value
-    if (!attr_set) {
-      const hipError_t ea =
-          hipFuncSetAttribute((const void*)pbl::k_lmhead_lds, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)((pbl::TM * (pbl::LDS_HMAX + 8) + pbl::LW_WAVES * pbl::TM * pbl::LROW) * 2));
-      if (ea != hipSuccess)
-        return pbs::report_errorf(PBS_ERR_HIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(ea));
-      attr_set = true;
+    const size_t lds = std::max(pbl::lds_hidden_bytes((int)hidden_dim), pbl::LDS_TILES);
+    if (lds > 64 * 1024) {
+      const int rc = lds_attribute();
+      if (rc != PBS_OK) return rc;
     }
     hipLaunchKernelGGL(pbl::k_lmhead_lds, dim3((ntiles + pbl::LW_WAVES - 1) / pbl::LW_WAVES),
                        dim3(64 * pbl::LW_WAVES), lds, (hipStream_t)stream, a);
