@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <utility>
 
 #include "pblmhead.h"
 #include "pbsample.h"
@@ -308,9 +309,10 @@ constexpr int LDS_HMAX = 1024;  // largest hidden_dim of this kernel
 constexpr size_t lds_hidden_bytes(int hdim) { return (size_t)TM * (size_t)(hdim + 8) * 2; }
 constexpr size_t LDS_TILES = (size_t)LW_WAVES * TM * TST * 4;
 
-// weight-only fragments and accumulators of one wave
+// weight-only fragments and accumulators of one wave, D weight chunks in flight
+template <int D>
 struct FragsW {
-  u4 w[WD][2][4];
+  u4 w[D][2][4];
   f32x16 acc[2][2];
 };
 
@@ -323,10 +325,10 @@ __device__ __forceinline__ void lds_frags(const uint16_t* hb, int hs, int r32, i
       h[t][s] = *(const u4*)(hb + (32 * t + r32) * hs + kc * KC + 32 * half + 8 * s);
 }
 
-template <int I, bool LW>
-__device__ __forceinline__ void kstep_lds(FragsW& f, __amdgpu_buffer_rsrc_t wrs, const uint32_t (&woff)[2],
+template <int D, int I, bool LW>
+__device__ __forceinline__ void kstep_lds(FragsW<D>& f, __amdgpu_buffer_rsrc_t wrs, const uint32_t (&woff)[2],
                                           const uint16_t* hb, int hs, int r32, int half, int kc) {
-  constexpr int B = I % WD;
+  constexpr int B = I % D;
   u4 h[2][4];
   lds_frags(hb, hs, r32, half, kc, h);
   __builtin_amdgcn_sched_barrier(0);  // all eight LDS reads go out before the first multiply
@@ -342,20 +344,37 @@ __device__ __forceinline__ void kstep_lds(FragsW& f, __amdgpu_buffer_rsrc_t wrs,
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (LW) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)((kc + WD) * KC * 2), f.w[B][t]);
+    for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)((kc + D) * KC * 2), f.w[B][t]);
   }
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int R, int I = 0>
-__device__ __forceinline__ void ktail_lds(FragsW& f, __amdgpu_buffer_rsrc_t wrs, const uint32_t (&woff)[2],
-                                          const uint16_t* hb, int hs, int r32, int half, int kc0) {
-  if constexpr (I < R) {
-    kstep_lds<I, (I + WD < R)>(f, wrs, woff, hb, hs, r32, half, kc0 + I);
-    ktail_lds<R, I + 1>(f, wrs, woff, hb, hs, r32, half, kc0);
+// chunks kc0 .. kc0 + D - 1 of a group (another group follows: every refill is valid)
+template <int D, int I = 0>
+__device__ __forceinline__ void kgroup_lds(FragsW<D>& f, __amdgpu_buffer_rsrc_t wrs, const uint32_t (&woff)[2],
+                                           const uint16_t* hb, int hs, int r32, int half, int kc0) {
+  if constexpr (I < D) {
+    kstep_lds<D, I, true>(f, wrs, woff, hb, hs, r32, half, kc0 + I);
+    kgroup_lds<D, I + 1>(f, wrs, woff, hb, hs, r32, half, kc0);
   }
 }
 
+// the last R chunks (D <= R < 2 D, or R = the whole row when it has fewer than 2 D)
+template <int D, int R, int I = 0>
+__device__ __forceinline__ void ktail_lds(FragsW<D>& f, __amdgpu_buffer_rsrc_t wrs, const uint32_t (&woff)[2],
+                                          const uint16_t* hb, int hs, int r32, int half, int kc0) {
+  if constexpr (I < R) {
+    kstep_lds<D, I, (I + D < R)>(f, wrs, woff, hb, hs, r32, half, kc0 + I);
+    ktail_lds<D, R, I + 1>(f, wrs, woff, hb, hs, r32, half, kc0);
+  }
+}
+
+// D weight chunks in flight per wave: the launch takes the largest of 1, 2, 4 that is at
+// most the row's chunk count nk, so every chunk of the prologue is one the wave
+// multiplies (four measured fastest at hidden_dim 576: three, five, six and eight were
+// 2-20 % slower); R = D + nk % D is the length of the last group. One tail per kernel: tails
+// of several lengths in one kernel make the register allocation of every path worse.
+template <int D, int R>
 __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
   // the hidden block while the waves multiply, then (after a barrier) the waves' fp32
   // tiles over it
@@ -379,7 +398,7 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
   for (int t = 0; t < 2; ++t) woff[t] = (uint32_t)((((int64_t)(n0 + 32 * t + r32)) * a.hdim + 32 * half) * 2);
 
   for (int m0 = 0; m0 < a.rows; m0 += TM) {
-    FragsW f;
+    FragsW<D> f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -425,34 +444,35 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
       u4 v[SB];
       batch_loads(q0, v);
 #pragma unroll
-      for (int d = 0; d < WD; ++d)
+      for (int d = 0; d < D; ++d)
 #pragma unroll
         for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
       batch_stores(q0, v);
     }
     __syncthreads();
     if (active) {
+      // whole groups of D chunks while another group follows them, then the last R
       int kc0 = 0;
-      for (; kc0 + 2 * WD <= nk; kc0 += WD) {
-        kstep_lds<0, true>(f, wrs, woff, hb, hs, r32, half, kc0);
-        kstep_lds<1, true>(f, wrs, woff, hb, hs, r32, half, kc0 + 1);
-        kstep_lds<2, true>(f, wrs, woff, hb, hs, r32, half, kc0 + 2);
-        kstep_lds<3, true>(f, wrs, woff, hb, hs, r32, half, kc0 + 3);
-      }
-      switch (nk - kc0) {
-        case 1: ktail_lds<1>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-        case 2: ktail_lds<2>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-        case 3: ktail_lds<3>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-        case 4: ktail_lds<4>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-        case 5: ktail_lds<5>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-        case 6: ktail_lds<6>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-        default: ktail_lds<7>(f, wrs, woff, hb, hs, r32, half, kc0); break;
-      }
+      for (; kc0 + 2 * D <= nk; kc0 += D) kgroup_lds<D>(f, wrs, woff, hb, hs, r32, half, kc0);
+      ktail_lds<D, R>(f, wrs, woff, hb, hs, r32, half, kc0);
     }
     __syncthreads();  // every wave's hidden reads are done: the tiles overwrite the block
     if (active) epilogue(a, tile, f.acc, m0, n0, tile_id, ntiles, l, half, r32);
     __syncthreads();  // the tiles are read before the next row block's hidden block
   }
+}
+
+// the k_lmhead_lds instantiation for a row of nk chunks (1 <= nk <= LDS_HMAX / KC)
+template <int D, int... Rs>
+constexpr const void* lds_kernel_for(int r, std::integer_sequence<int, Rs...>) {
+  const void* k = nullptr;
+  ((k = (r == D + Rs) ? (const void*)k_lmhead_lds<D, D + Rs> : k), ...);
+  return k;
+}
+inline const void* lds_kernel(int nk) {
+  if (nk >= 4) return lds_kernel_for<4>(4 + nk % 4, std::make_integer_sequence<int, 4>{});
+  if (nk >= 2) return lds_kernel_for<2>(2 + nk % 2, std::make_integer_sequence<int, 2>{});
+  return (const void*)k_lmhead_lds<1, 1>;
 }
 
 // One workgroup of 256 threads per row: the largest of the row's tile keys (up to four
@@ -503,6 +523,7 @@ std::mutex g_scratch_mu;
 void* g_scratch_dev[MAX_DEVICES];  // scratch's device address on each GPU (null until its first call)
 
 // k_lmhead_lds may take more than 64 KiB of dynamic LDS: raise its limit once per device
+// (every instantiation)
 std::atomic<bool> g_lds_attr[MAX_DEVICES];
 
 int lds_attribute() {
@@ -511,9 +532,12 @@ int lds_attribute() {
   if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= MAX_DEVICES) return pbs::report_errorf(PBS_ERR_HIP, "device index %d out of range", dev);
   if (g_lds_attr[dev].load(std::memory_order_acquire)) return PBS_OK;
-  e = hipFuncSetAttribute((const void*)pbl::k_lmhead_lds, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)std::max(pbl::lds_hidden_bytes(pbl::LDS_HMAX), pbl::LDS_TILES));
-  if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+  for (int nk = 1; nk <= pbl::LDS_HMAX / pbl::KC; ++nk) {
+    e = hipFuncSetAttribute(pbl::lds_kernel(nk), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)std::max(pbl::lds_hidden_bytes(pbl::LDS_HMAX), pbl::LDS_TILES));
+    if (e != hipSuccess)
+      return pbs::report_errorf(PBS_ERR_HIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+  }
   g_lds_attr[dev].store(true, std::memory_order_release);
   return PBS_OK;
 }
@@ -582,8 +606,11 @@ int pbs_lm_head_argmax(const uint16_t* hidden, int64_t hidden_stride, const uint
       const int rc = lds_attribute();
       if (rc != PBS_OK) return rc;
     }
-    hipLaunchKernelGGL(pbl::k_lmhead_lds, dim3((ntiles + pbl::LW_WAVES - 1) / pbl::LW_WAVES),
-                       dim3(64 * pbl::LW_WAVES), lds, (hipStream_t)stream, a);
+    const dim3 grid((ntiles + pbl::LW_WAVES - 1) / pbl::LW_WAVES), block(64 * pbl::LW_WAVES);
+    void* args[] = {&a};
+    const hipError_t el = hipLaunchKernel(pbl::lds_kernel((int)(hidden_dim / pbl::KC)), grid, block, args, lds,
+                                          (hipStream_t)stream);
+    if (el != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(el));
   } else {
     hipLaunchKernelGGL(pbl::k_lmhead, dim3(ntiles), dim3(64), 0, (hipStream_t)stream, a);
   }

@@ -79,6 +79,11 @@ def check(dev, rows, hdim, vocab, seed, scale=1.0, plant=None):
     (100, 576, 4099),   # two row blocks, the second partial
     (33, 64, 65),
     (130, 192, 2048),   # three row blocks
+    (5, 256, 300),      # 4 chunks of 64: four in flight, a last group of four
+    (9, 384, 777),      # 6 chunks: a last group of six
+    (3, 448, 129),      # 7 chunks: a last group of seven
+    (17, 960, 1500),    # 15 chunks: two groups, then seven
+    (70, 1024, 640),    # the largest LDS-resident hidden block, two row blocks
     (8, 1088, 3000),    # hidden_dim past the LDS-resident limit: the L2-fragment kernel
     (65, 2048, 700),
 ])
