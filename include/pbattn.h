@@ -37,7 +37,8 @@ extern "C" {
  *   max_context   host bound on every context_lens[b] (sizes the kernel's LDS)
  *   out           device float[rows][n_heads][head_dim]
  * head_dim must be 64, n_heads a multiple of n_kv_heads with at most 8 query heads per
- * KV head, max_context <= 2048 (EngineConfig.max_model_len's default), n_slots < 2^31. A slot outside [0, n_slots) (a corrupt block table)
+ * KV head, max_context <= 2048 (EngineConfig.max_model_len's default), n_slots < 2^31; q,
+ * k_cache and v_cache 16-byte aligned. A slot outside [0, n_slots) (a corrupt block table)
  * makes that sequence's output NaN instead of reading out of bounds. Returns 0 or a
  * negative PBS_ERR_* code (pbs_last_error() says why); asynchronous on `stream`.
  */

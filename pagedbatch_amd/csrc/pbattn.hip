@@ -1,19 +1,20 @@
 // Paged-attention decode kernel for gfx950 (CDNA4), part of libpbsample.so.
 //
 // One decode step of grouped-query attention over a paged KV cache
-// (pagedbatch/model.py:201-224): one workgroup per (sequence, KV head) reads each K and
-// V row of that head once and serves the n_rep query heads that share it.
+// (pagedbatch/model.py:201-224): one workgroup of four waves per (sequence, KV head) reads
+// each K and V row of that head once and serves the n_rep query heads that share it.
 //
-//   1. The query rows of the group go to LDS; every thread takes context positions
-//      t = tid, tid + 256, ...: its slot through the block table
-//      (pagedbatch/block_manager.py:88-91), the K row (64 bf16, eight 16-byte loads) and
-//      the n_rep scaled dot products, in fp32, into an LDS score table.
-//   2. Per query head: the maximum and the sum of exp(score - max) (block reductions).
-//   3. V rows in tiles of 256 positions staged through LDS (eight independent 16-byte
-//      loads per thread), then threads (position group, dim) accumulate
-//      sum_t p[t] * V[t][dim] for every query head.
-// Memory: (K + V) * context * 128 B per (sequence, KV head), read once; HBM-bound for
-// long contexts, launch- and latency-bound for short ones.
+// Each wave takes chunks of 64 context positions (wave w: chunks w, w + 4, ...). Lane l
+// holds 8 of the 64 dims (8 (l % 8) ..) of 8 positions (8 j + l / 8, j < 8): its slots
+// through the block table (pagedbatch/block_manager.py:88-91), then the K and V pieces of
+// those rows, all issued together (16-byte loads, eight lanes per 128-byte row). The eight
+// lanes of a position finish its dot products with three DPP steps, which leaves the scores
+// in the lanes that hold the matching V pieces, so the weighted sum needs no exchange.
+// Each wave keeps an online softmax (running maximum, sum and weighted V sum per query
+// head); the four waves meet once in LDS at the end. fp32 throughout.
+// Memory: (K + V) * context * 128 B per (sequence, KV head), read once; at decode batch
+// sizes the kernel is latency-bound: two dependent loads (block table, then K and V) and
+// one barrier.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -28,9 +29,11 @@ int report_error(int code, const char* msg);
 namespace pba {
 
 constexpr int NT = 256;
+constexpr int NW = NT / 64;  // waves per workgroup
 constexpr int D = 64;
 constexpr int MAX_REP = 8;
 constexpr int MAX_CONTEXT = 2048;
+constexpr int QUAD_XOR1 = 0xb1, QUAD_XOR2 = 0x4e, ROW_HALF_MIRROR = 0x141;
 
 struct Args {
   const float* q;
@@ -48,156 +51,180 @@ struct Args {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// N values at once, max or sum over the workgroup: shuffles inside each wave, then the
-// waves' results through LDS (red: [NT / 64][N]); every thread gets the totals
-template <bool MAX, int N>
-__device__ __forceinline__ void block_reduce_n(float (&v)[N], float* red) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    for (int off = 32; off > 0; off >>= 1) {
-      const float o = __shfl_xor(v[i], off, 64);
-      v[i] = MAX ? fmaxf(v[i], o) : v[i] + o;
-    }
-  }
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) red[w * N + i] = v[i];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    float r = red[i];
-    for (int ww = 1; ww < NT / 64; ++ww) r = MAX ? fmaxf(r, red[ww * N + i]) : r + red[ww * N + i];
-    v[i] = r;
-  }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 
+// sum over the 8 lanes of a group (lanes 8 g .. 8 g + 7): quad swaps, then the half-row
+// mirror pairs quad 0 of the group with quad 1; every lane ends with the total
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp_f<QUAD_XOR1>(v);
+  v += dpp_f<QUAD_XOR2>(v);
+  return v + dpp_f<ROW_HALF_MIRROR>(v);
+}
+
+// across the 8 groups of a wave (lanes l, l ^ 8, ..., l ^ 56)
+__device__ __forceinline__ float groups_max(float v) {
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float groups_sum(float v) {
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int REP>
 __global__ __launch_bounds__(NT) void k_decode(Args a) {
-  extern __shared__ float lds[];
-  uint4* vt = (uint4*)lds;                           // [NT][D / 8]: a tile of V rows
-  float* qs = (float*)(vt + NT * (D / 8));           // [rep][D]
-  float* red = qs + MAX_REP * D;                     // [NT / 64][MAX_REP + 1]
-  float* part = red + (NT / 64) * (MAX_REP + 1);     // [NT / D][MAX_REP][D] partial sums
-  int* slot_s = (int*)(part + (NT / D) * MAX_REP * D);  // [max_context]
-  float* sc = (float*)(slot_s + a.max_context);      // [rep][max_context]
+  __shared__ float m_s[NW][MAX_REP], s_s[NW][MAX_REP];
+  __shared__ float acc_s[NW][MAX_REP][D];
+  __shared__ int bad_s[NW];
 
   const int b = blockIdx.x / a.n_kv_heads;
   const int kvh = blockIdx.x % a.n_kv_heads;
-  const int rep = a.rep;
   const int L = a.context_lens[b];
-  const int tid = threadIdx.x;
-  float* out = a.out + ((size_t)b * a.n_heads + (size_t)kvh * rep) * D;
+  const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+  const int g = l >> 3, e0 = 8 * (l & 7);
+  float* out = a.out + ((size_t)b * a.n_heads + (size_t)kvh * REP) * D;
   if (L < 1 || L > a.max_context) {  // out of the declared range: no reads, NaN out
-    for (int i = tid; i < rep * D; i += NT) out[i] = __int_as_float(0x7fc00000);
+    for (int i = tid; i < REP * D; i += NT) out[i] = __int_as_float(0x7fc00000);
     return;
   }
-  for (int i = tid; i < rep * D; i += NT) qs[i] = a.q[((size_t)b * a.n_heads + (size_t)kvh * rep) * D + i];
-  __syncthreads();
+  // the lane's 8 dims of every query head of the group
+  float qv[REP][8];
+  {
+    const float4* qp = (const float4*)(a.q + ((size_t)b * a.n_heads + (size_t)kvh * REP) * D + e0);
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      const float4 x0 = qp[h * (D / 4)], x1 = qp[h * (D / 4) + 1];
+      qv[h][0] = x0.x, qv[h][1] = x0.y, qv[h][2] = x0.z, qv[h][3] = x0.w;
+      qv[h][4] = x1.x, qv[h][5] = x1.y, qv[h][6] = x1.z, qv[h][7] = x1.w;
+    }
+  }
+  // position p -> (block index, offset): (p + 0.5) * fl(1 / block_size) is within
+  // (p + 0.5) * 2^-23 of the exact quotient, below its 0.5 / block_size distance from an
+  // integer for every p < 2^22, so the truncation is exact
+  const float inv_bs = 1.0f / (float)a.block_size;
+  const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
 
-  // 1. scores
+  float m_run[REP], s_run[REP], acc[REP][8];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    m_run[h] = -__builtin_inff();
+    s_run[h] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+  }
   int bad = 0;
-  float mx[MAX_REP];
+  for (int t0 = 64 * w; t0 < L; t0 += 64 * NW) {
+    // slots of the lane's positions t0 + 8 j + g (positions past the context read slot 0,
+    // a bad block-table entry reads slot 0 and marks the sequence)
+    int64_t row[8];
 #pragma unroll
-  for (int h = 0; h < MAX_REP; ++h) mx[h] = -INFINITY;
-  for (int t = tid; t < L; t += NT) {
-    const int64_t blk = a.block_table[(size_t)b * a.max_blocks + t / a.block_size];
-    const int64_t slot = blk * a.block_size + t % a.block_size;
-    const bool ok = blk >= 0 && slot >= 0 && slot < a.n_slots;
-    bad |= ok ? 0 : 1;
-    slot_s[t] = ok ? (int)slot : -1;
-    float acc[MAX_REP];
-#pragma unroll
-    for (int h = 0; h < MAX_REP; ++h) acc[h] = 0.0f;
-    if (ok) {
-      const uint4* kr = (const uint4*)(a.k + ((size_t)slot * a.n_kv_heads + kvh) * D);
-#pragma unroll
-      for (int c = 0; c < D / 8; ++c) {
-        const uint4 w = kr[c];
-        const float kv[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
-                             bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
-#pragma unroll
-        for (int h = 0; h < MAX_REP; ++h) {
-          if (h < rep) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h] = fmaf(qs[h * D + c * 8 + e], kv[e], acc[h]);
-          }
-        }
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int pos = t0 + 8 * j + g;
+      const int bi = (int)(((float)pos + 0.5f) * inv_bs);
+      const int32_t blk = pos < L ? bt[bi] : 0;
+      const int64_t slot = (int64_t)blk * a.block_size + (pos - bi * a.block_size);
+      const bool ok = blk >= 0 && slot < a.n_slots;
+      bad |= (pos < L && !ok) ? 1 : 0;
+      row[j] = ((ok && pos < L) ? slot : 0) * a.n_kv_heads + kvh;
     }
+    uint4 kq[8], vq[8];
 #pragma unroll
-    for (int h = 0; h < MAX_REP; ++h) {
-      if (h < rep) {
-        const float sv = acc[h] * a.scale;
-        sc[h * a.max_context + t] = sv;
-        mx[h] = fmaxf(mx[h], sv);
-      }
-    }
-  }
-  // 2. one block reduction for every head's maximum and the corrupt-slot flag, one for
-  //    every head's sum of exponentials (the weights replace the scores in place)
-  float mv[MAX_REP + 1];
+    for (int j = 0; j < 8; ++j) kq[j] = *(const uint4*)(a.k + row[j] * D + e0);
 #pragma unroll
-  for (int h = 0; h < MAX_REP; ++h) mv[h] = mx[h];
-  mv[MAX_REP] = bad ? 1.0f : 0.0f;
-  block_reduce_n<true>(mv, red);
-  if (mv[MAX_REP] > 0.0f) {  // a corrupt slot anywhere in the context: NaN out
-    for (int i = tid; i < rep * D; i += NT) out[i] = __int_as_float(0x7fc00000);
-    return;
-  }
-  float sum[MAX_REP + 1];
-#pragma unroll
-  for (int h = 0; h <= MAX_REP; ++h) sum[h] = 0.0f;
-  for (int t = tid; t < L; t += NT) {
-#pragma unroll
-    for (int h = 0; h < MAX_REP; ++h) {
-      if (h < rep) {
-        const float e = __expf(sc[h * a.max_context + t] - mv[h]);
-        sc[h * a.max_context + t] = e;
-        sum[h] += e;
-      }
-    }
-  }
-  block_reduce_n<false>(sum, red);
+    for (int j = 0; j < 8; ++j) vq[j] = *(const uint4*)(a.v + row[j] * D + e0);
 
-  // 3. weighted sum of the V rows, in tiles of NT positions staged through LDS (every
-  //    thread issues its eight 16-byte loads of a tile at once); thread (q4, d) then takes
-  //    dim d and the tile's positions q4, q4 + 4, ... for every query head (one V element
-  //    read serves them all); the four position groups' partial sums meet in LDS
-  const int d = tid & (D - 1), q4 = tid >> 6;
-  float acc[MAX_REP];
+    // scores of the lane's 8 positions for every head (-inf past the context)
+    float sc[REP][8];
 #pragma unroll
-  for (int h = 0; h < MAX_REP; ++h) acc[h] = 0.0f;
-  for (int t0 = 0; t0 < L; t0 += NT) {
-    const int n = min(NT, L - t0);
-    __syncthreads();  // the previous tile is consumed
+    for (int j = 0; j < 8; ++j) {
+      const float kv[8] = {bf16_lo(kq[j].x), bf16_hi(kq[j].x), bf16_lo(kq[j].y), bf16_hi(kq[j].y),
+                           bf16_lo(kq[j].z), bf16_hi(kq[j].z), bf16_lo(kq[j].w), bf16_hi(kq[j].w)};
 #pragma unroll
-    for (int i0 = 0; i0 < NT * (D / 8); i0 += NT) {
-      const int i = i0 + tid, r = i >> 3;
-      if (r < n) vt[i] = ((const uint4*)(a.v + ((size_t)slot_s[t0 + r] * a.n_kv_heads + kvh) * D))[i & 7];
+      for (int h = 0; h < REP; ++h) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qv[h][e], kv[e], d);
+        d = group8_sum(d) * a.scale;
+        sc[h][j] = (t0 + 8 * j + g < L) ? d : -__builtin_inff();
+      }
     }
-    __syncthreads();
-    for (int r = q4; r < n; r += NT / D) {
-      const float vv = __uint_as_float((uint32_t)((const uint16_t*)(vt + r * (D / 8)))[d] << 16);
+    // online softmax update of every head
 #pragma unroll
-      for (int h = 0; h < MAX_REP; ++h)
-        if (h < rep) acc[h] = fmaf(sc[h * a.max_context + t0 + r], vv, acc[h]);
+    for (int h = 0; h < REP; ++h) {
+      float mc = sc[h][0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) mc = fmaxf(mc, sc[h][j]);
+      mc = groups_max(mc);
+      const float mn = fmaxf(m_run[h], mc);  // finite: the chunk holds a position < L
+      const float alpha = __expf(m_run[h] - mn);
+      m_run[h] = mn;
+      float ps = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pj = __expf(sc[h][j] - mn);
+        ps += pj;
+        const uint4 vw = vq[j];
+        acc[h][0] = fmaf(pj, bf16_lo(vw.x), acc[h][0]);
+        acc[h][1] = fmaf(pj, bf16_hi(vw.x), acc[h][1]);
+        acc[h][2] = fmaf(pj, bf16_lo(vw.y), acc[h][2]);
+        acc[h][3] = fmaf(pj, bf16_hi(vw.y), acc[h][3]);
+        acc[h][4] = fmaf(pj, bf16_lo(vw.z), acc[h][4]);
+        acc[h][5] = fmaf(pj, bf16_hi(vw.z), acc[h][5]);
+        acc[h][6] = fmaf(pj, bf16_lo(vw.w), acc[h][6]);
+        acc[h][7] = fmaf(pj, bf16_hi(vw.w), acc[h][7]);
+      }
+      s_run[h] = s_run[h] * alpha + ps;
     }
   }
+  // the wave's totals: the 8 groups hold disjoint positions (the lanes of a group hold the
+  // same ones); waves without a position keep m = -inf, s = 0, acc = 0
 #pragma unroll
-  for (int h = 0; h < MAX_REP; ++h)
-    if (h < rep) part[(q4 * MAX_REP + h) * D + d] = acc[h];
+  for (int h = 0; h < REP; ++h) {
+    s_run[h] = groups_sum(s_run[h]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = groups_sum(acc[h][e]);
+  }
+  const bool wave_bad = __any(bad);
+  if (l < 8) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc_s[w][h][e0 + e] = acc[h][e];
+      if (l == 0) {
+        m_s[w][h] = m_run[h];
+        s_s[w][h] = s_run[h];
+      }
+    }
+    if (l == 0) bad_s[w] = wave_bad ? 1 : 0;
+  }
   __syncthreads();
-  for (int p = tid; p < rep * D; p += NT) {
-    const int h = p / D, dd = p % D;
-    float tot = 0.0f;
+  bool any_bad = false;
 #pragma unroll
-    for (int g = 0; g < NT / D; ++g) tot += part[(g * MAX_REP + h) * D + dd];
-    float s = 1.0f;
+  for (int ww = 0; ww < NW; ++ww) any_bad |= bad_s[ww] != 0;
+  for (int i = tid; i < REP * D; i += NT) {
+    const int h = i / D, d = i % D;
+    if (any_bad) {  // a corrupt slot anywhere in the context: NaN out
+      out[i] = __int_as_float(0x7fc00000);
+      continue;
+    }
+    float mx = m_s[0][h];
 #pragma unroll
-    for (int hh = 0; hh < MAX_REP; ++hh) s = (hh == h) ? sum[hh] : s;
-    out[p] = tot / s;
+    for (int ww = 1; ww < NW; ++ww) mx = fmaxf(mx, m_s[ww][h]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = __expf(m_s[ww][h] - mx);  // 0 for a wave without positions
+      num = fmaf(f, acc_s[ww][h][d], num);
+      den = fmaf(f, s_s[ww][h], den);
+    }
+    out[i] = num / den;
   }
 }
 
@@ -222,8 +249,10 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT,
                              "max_context must be in [1, 2048] and covered by max_blocks * block_size");
   if (rows * n_kv_heads > 0x7fffffff) return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "too many rows");
-  if (n_slots > 0x7fffffff)  // slot numbers are kept as 32-bit ints in LDS
+  if (n_slots > 0x7fffffff)
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "n_slots must be below 2^31");
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u)
+    return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "q, k_cache and v_cache must be 16-byte aligned");
   Args a;
   a.q = q;
   a.k = k_cache;
@@ -239,14 +268,18 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
   a.max_context = max_context;
   a.scale = scale;
   a.out = out;
-  const size_t lds = sizeof(uint4) * NT * (D / 8) +
-                     sizeof(float) * (MAX_REP * D + (NT / 64) * (MAX_REP + 1) + (NT / D) * MAX_REP * D) +
-                     sizeof(int) * max_context + sizeof(float) * (size_t)a.rep * max_context;
-  if (lds > 64 * 1024) {
-    const hipError_t ea = hipFuncSetAttribute((const void*)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (ea != hipSuccess) return pbs::report_error(PBS_ERR_HIP, hipGetErrorString(ea));
+  const dim3 grid((unsigned)(rows * n_kv_heads)), block(NT);
+  hipStream_t st = (hipStream_t)stream;
+  switch (a.rep) {
+    case 1: hipLaunchKernelGGL(k_decode<1>, grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_decode<2>, grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL(k_decode<3>, grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL(k_decode<4>, grid, block, 0, st, a); break;
+    case 5: hipLaunchKernelGGL(k_decode<5>, grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL(k_decode<6>, grid, block, 0, st, a); break;
+    case 7: hipLaunchKernelGGL(k_decode<7>, grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL(k_decode<8>, grid, block, 0, st, a); break;
   }
-  hipLaunchKernelGGL(k_decode, dim3((unsigned)(rows * n_kv_heads)), dim3(NT), lds, (hipStream_t)stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return pbs::report_error(PBS_ERR_HIP, hipGetErrorString(e));
   return PBS_OK;

@@ -522,23 +522,22 @@ constexpr int MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[MAX_DEVICES];  // scratch's device address on each GPU (null until its first call)
 
-// k_lmhead_lds may take more than 64 KiB of dynamic LDS: raise its limit once per device
-// (every instantiation)
-std::atomic<bool> g_lds_attr[MAX_DEVICES];
+// k_lmhead_lds may take more than 64 KiB of dynamic LDS: raise the limit of the kernel for
+// nk chunks once per device, on its first launch there (the first attribute call on a
+// kernel loads its code, so the others are left alone)
+constexpr int LDS_KERNELS = pbl::LDS_HMAX / pbl::KC;
+std::atomic<bool> g_lds_attr[MAX_DEVICES][LDS_KERNELS + 1];
 
-int lds_attribute() {
+int lds_attribute(int nk) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= MAX_DEVICES) return pbs::report_errorf(PBS_ERR_HIP, "device index %d out of range", dev);
-  if (g_lds_attr[dev].load(std::memory_order_acquire)) return PBS_OK;
-  for (int nk = 1; nk <= pbl::LDS_HMAX / pbl::KC; ++nk) {
-    e = hipFuncSetAttribute(pbl::lds_kernel(nk), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)std::max(pbl::lds_hidden_bytes(pbl::LDS_HMAX), pbl::LDS_TILES));
-    if (e != hipSuccess)
-      return pbs::report_errorf(PBS_ERR_HIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
-  }
-  g_lds_attr[dev].store(true, std::memory_order_release);
+  if (g_lds_attr[dev][nk].load(std::memory_order_acquire)) return PBS_OK;
+  e = hipFuncSetAttribute(pbl::lds_kernel(nk), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)std::max(pbl::lds_hidden_bytes(pbl::LDS_HMAX), pbl::LDS_TILES));
+  if (e != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+  g_lds_attr[dev][nk].store(true, std::memory_order_release);
   return PBS_OK;
 }
 
@@ -603,7 +602,7 @@ int pbs_lm_head_argmax(const uint16_t* hidden, int64_t hidden_stride, const uint
   if (hidden_dim <= pbl::LDS_HMAX) {
     const size_t lds = std::max(pbl::lds_hidden_bytes((int)hidden_dim), pbl::LDS_TILES);
     if (lds > 64 * 1024) {
-      const int rc = lds_attribute();
+      const int rc = lds_attribute((int)(hidden_dim / pbl::KC));
       if (rc != PBS_OK) return rc;
     }
     const dim3 grid((ntiles + pbl::LW_WAVES - 1) / pbl::LW_WAVES), block(64 * pbl::LW_WAVES);

@@ -334,6 +334,8 @@ def _attn(lib, **kw):
     ({"maxc": 5000, "max_blocks": 400}, "max_context"),
     ({"bs": 0}, "block_size"),
     ({"n_slots": 1 << 31}, "n_slots"),
+    ({"q": (1 << 20) + 4}, "16-byte aligned"),
+    ({"v": (1 << 20) + 8}, "16-byte aligned"),
 ])
 def test_attention_abi_rejects_bad_arguments(kw, msg):
     lib = _lib.load()
