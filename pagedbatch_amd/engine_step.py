@@ -293,10 +293,12 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
             for j, i in enumerate(stoch):
                 toks[i], reasons[i] = st[j], sr[j]
         if greedy:
-            gsel = gtok[torch.tensor(greedy, device=gtok.device)]
-            gr = finish_reasons(gsel, [rule] * len(greedy), None, prompt_len + output_len)
-            for j, (i, t) in enumerate(zip(greedy, gsel.cpu().tolist())):
-                toks[i], reasons[i] = t, gr[j]
+            # the stop check over every row's greedy token (as cheap as over the greedy rows,
+            # and no device gather), then the greedy rows' entries on the host
+            gr = finish_reasons(gtok, [rule] * num_seqs, None, prompt_len + output_len)
+            gl = gtok.cpu().tolist()
+            for i in greedy:
+                toks[i], reasons[i] = gl[i], gr[i]
         return toks, reasons
 
     toks = step(0, prompts.to(device), 0, prompt_len)

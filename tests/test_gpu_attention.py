@@ -54,6 +54,50 @@ def test_decode_matches_torch(B, Hq, Hkv, bs, maxL, seed):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed", [(4, 9, 3, 16, 200, 11), (3, 8, 2, 16, 700, 12), (2, 4, 4, 8, 1, 13)])
+def test_decode_matches_reference_bf16_sdpa(B, Hq, Hkv, bs, maxL, seed):
+    """Against the reference's own arithmetic (model.py:212-222): bf16 q, K and V gathered
+    through the slot table, the KV heads repeated, F.scaled_dot_product_attention in bf16
+    (on the CPU). The kernel computes in fp32 from the same bf16 inputs; torch's bf16 result
+    differs from the exact one by at most a bf16 rounding of the weights and one of the
+    output, so the bar is 2^-8 * (max |v| + |out|) per element."""
+    import torch.nn.functional as F
+
+    from pagedbatch_amd.attention import decode_attention
+
+    print(f"[case] decode vs bf16 sdpa B={B} Hq={Hq} Hkv={Hkv} bs={bs} maxL={maxL}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    D = 64
+    nblk = (maxL + bs - 1) // bs
+    n_slots = B * nblk * bs + bs
+    kc = (torch.randn(n_slots, Hkv, D, generator=g) * 0.5).to(torch.bfloat16)
+    vc = torch.randn(n_slots, Hkv, D, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(n_slots // bs, generator=g)[: B * nblk].view(B, nblk).to(torch.int32)
+    lens = torch.randint(1, maxL + 1, (B,), generator=g).to(torch.int32)
+    lens[0] = maxL
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    rep = Hq // Hkv
+    want = torch.empty(B, Hq, D)
+    bound = torch.empty(B, Hq, D)
+    for b in range(B):
+        L = int(lens[b])
+        t = torch.arange(L)
+        slots = perm[b, t // bs].long() * bs + t % bs
+        keys = kc[slots].repeat_interleave(rep, dim=1).transpose(0, 1).unsqueeze(0)  # [1, Hq, L, D]
+        values = vc[slots].repeat_interleave(rep, dim=1).transpose(0, 1).unsqueeze(0)
+        o = F.scaled_dot_product_attention(q[b].view(1, Hq, 1, D), keys, values).view(Hq, D).float()
+        want[b] = o
+        vmax = values.float().abs().amax(dim=(2, 3)).view(Hq, 1)  # per head
+        bound[b] = 2.0 ** -8 * (vmax + o.abs())
+    dev = torch.device("cuda", 0)
+    got = decode_attention(q.float().to(dev), kc.to(dev), vc.to(dev), perm.to(dev), lens.to(dev), bs, maxL).cpu()
+    err = (got - want).abs()
+    assert bool((err <= bound).all()), f"max err / bar {float((err / bound).max()):.3f}"
+    if maxL == 1:  # a single position: the output is that V row, exactly
+        assert torch.equal(got, want)
+
+
+@pytest.mark.gpu
 def test_decode_corrupt_block_table_gives_nan_not_a_fault():
     from pagedbatch_amd.attention import decode_attention
 
