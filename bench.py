@@ -301,8 +301,9 @@ def lm_head_bench(args):
 def engine_step(args):
     """The end-to-end engine step (smollm2-135m-random, 64 requests x 128 prompt + 128
     output tokens, half greedy, half top-k=50 / top-p=0.9): decode throughput (`value`:
-    batched sampling and the paged-attention decode kernel) and the sampler's share of
-    the step, with the batched call and with one call per row (torch attention)."""
+    the decode forward replayed from a HIP graph with the paged-attention decode kernel,
+    batched sampling) and the sampler's share of the step, also with the forward launched
+    op by op, with one sampling call per row (torch attention) and with the fused lm_head."""
     import torch
 
     from pagedbatch_amd import engine_step as es
@@ -321,6 +322,9 @@ def engine_step(args):
     sampler_kernel_us = engine_sampler_kernel_us(tf.captures[0])
     print("[bench] engine step: fused lm_head + greedy, paged-attention decode kernel", file=sys.stderr, flush=True)
     th, out_h = es.run(shape, **kw, fused_decode=True, fused_head=True)
+    print("[bench] engine step: decode forward replayed from a HIP graph, paged-attention decode kernel",
+          file=sys.stderr, flush=True)
+    tg, out_g = es.run(shape, **kw, fused_decode=True, graph=True)
     agree_head = sum(a == b for x, y in zip(out_f, out_h) for a, b in zip(x, y)) / sum(len(x) for x in out_f)
     # the fused attention rounds differently in the last fp32 bits, which the bf16 o_proj
     # input can turn into different tokens later in a sequence: report the agreement
@@ -334,8 +338,10 @@ def engine_step(args):
                 "sample_share": round(sum(smp) / (sum(fwd) + sum(smp)), 4),
                 "prefill_forward_ms": round(1e3 * t.forward_s[0], 3), "prefill_sample_ms": round(1e3 * t.sample_s[0], 4)}
 
-    b, r, f, hd = split(tb), split(tr), split(tf), split(th)
-    step_ms = f["forward_ms"] + f["sample_ms"]
+    b, r, f, hd, gr = split(tb), split(tr), split(tf), split(th), split(tg)
+    # the graph replays the eager fused step's kernels: the same tokens, or the graph is wrong
+    same_graph = out_g == out_f
+    step_ms = gr["forward_ms"] + gr["sample_ms"]
     # the batched call runs the stop check (engine.py:173-182) on the device after the
     # sampler and brings the reasons back with the tokens: every request ends on "length"
     # at its 128th output, none before
@@ -347,7 +353,9 @@ def engine_step(args):
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights, random prompt ids)",
         "config": {"workload": "engine_step_smollm2", "requests": 64, "prompt_len": 128, "output_len": 128,
                    "block_size": 16, "mix": "half greedy, half top_k=50 top_p=0.9 T=1.0",
-                   "decode_attention": "paged-attention kernel (pba_decode_attention)"},
+                   "decode_attention": "paged-attention kernel (pba_decode_attention)",
+                   "decode_forward": "HIP graph replay (engine_step.DecodeGraph)"},
+        "graph_decode": {**gr, "same_tokens_as_eager": same_graph},
         "fused_decode_attention": f, "batched_sampling": b, "per_row_sampling": r,
         "fused_lm_head": {**hd, "note": "forward ends at the final hidden state; sample_ms includes the lm_head "
                                         "GEMM (pbs_lm_head_argmax) and the stochastic rows' sampling",

@@ -100,17 +100,27 @@ class Model:
         return x * cos + rot * sin
 
     @torch.no_grad()
-    def forward(self, tokens: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor, seq_slots: torch.Tensor,
-                q_len: int, cache: "PagedKV", fused_decode: bool = False, hidden_only: bool = False) -> torch.Tensor:
+    def forward(self, tokens: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor, seq_slots: torch.Tensor | None,
+                q_len: int, cache: "PagedKV", fused_decode: bool = False, hidden_only: bool = False,
+                context_lens: torch.Tensor | None = None, max_context: int | None = None) -> torch.Tensor:
         """``tokens``/``pos``/``slots``: [B * q_len] (sequence-major); ``seq_slots``: [B, L] the
         cache slots of each sequence's whole context, new tokens last. Returns [B, vocab]
         logits of each sequence's last token (with ``hidden_only``, its final hidden state
         [B, hidden] instead, for the fused lm_head). ``fused_decode`` runs decode steps
         (``q_len == 1``) through the paged-attention kernel (``attention.decode_attention``)
-        instead of the gather + matmul + softmax below."""
+        instead of the gather + matmul + softmax below; it may take the context lengths as a
+        device tensor ``context_lens`` with a fixed bound ``max_context`` instead of
+        ``seq_slots`` (None), so that the step has the same shapes and kernel arguments every
+        time (a captured graph)."""
         s = self.shape
         D, Hq, Hkv = s.head_dim, s.num_heads, s.num_kv_heads
-        B, L = seq_slots.shape
+        if seq_slots is not None:
+            B, L = seq_slots.shape
+        else:
+            if not (fused_decode and q_len == 1 and context_lens is not None and max_context is not None):
+                raise ValueError("without seq_slots the step must be a fused decode step with context_lens and "
+                                 "max_context")
+            B, L = tokens.numel(), None
         x = self.embed[tokens]
         scale = 1.0 / math.sqrt(D)
         causal = None
@@ -127,9 +137,11 @@ class Model:
             cache.k[li].index_copy_(0, slots, k.to(cache.k[li].dtype))
             cache.v[li].index_copy_(0, slots, v)
             if fused_decode and q_len == 1:
-                o = decode_attention(q.contiguous(), cache.k[li], cache.v[li], cache.block_table_i32,
-                                     torch.full((B,), L, dtype=torch.int32, device=x.device), cache.block_size,
-                                     L, scale).view(B, Hq * D)
+                lens = context_lens if context_lens is not None else \
+                    torch.full((B,), L, dtype=torch.int32, device=x.device)
+                o = decode_attention(q.contiguous(), cache.k[li], cache.v[li], cache.block_table_i32, lens,
+                                     cache.block_size, max_context if max_context is not None else L,
+                                     scale).view(B, Hq * D)
             else:
                 # attention in fp32 with contiguous operands: [B, Hkv, rep, q_len, D] x [B, Hkv, D, L]
                 keys = cache.k[li][seq_slots].float().permute(0, 2, 3, 1).contiguous()  # [B, Hkv, D, L]
@@ -146,6 +158,49 @@ class Model:
             x = x + (F.silu(gu[:, : s.intermediate_size]) * gu[:, s.intermediate_size :]) @ p["down"]
         last = self._rms(x.view(B, q_len, -1)[:, -1], self.norm)
         return last.contiguous() if hidden_only else last @ self.head
+
+
+class DecodeGraph:
+    """The decode step's forward (one token per sequence, attention through the
+    paged-attention kernel) captured once in a HIP graph and replayed every step. The
+    per-step inputs (token ids, positions, cache slots, context lengths) live in fixed
+    device buffers refilled before each replay, and the replay overwrites one fixed output
+    buffer (the logits, or with ``hidden_only`` the final hidden state), which the caller
+    consumes before the next replay. The capture's warm-up steps write the cache at slot 0
+    with dummy values, so the graph is built before the prefill writes the prompts."""
+
+    def __init__(self, model: Model, cache: "PagedKV", num_seqs: int, max_context: int, hidden_only: bool):
+        dev = model.embed.device
+        self.tokens = torch.zeros(num_seqs, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(num_seqs, dtype=torch.long, device=dev)
+        self.slots = torch.zeros(num_seqs, dtype=torch.long, device=dev)
+        self.lens = torch.ones(num_seqs, dtype=torch.int32, device=dev)
+
+        def fwd():
+            return model.forward(self.tokens, self.pos, self.slots, None, 1, cache, fused_decode=True,
+                                 hidden_only=hidden_only, context_lens=self.lens, max_context=max_context)
+
+        # warm-up on a side stream (libraries pick their kernels and workspaces outside the
+        # capture), then the capture
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fwd()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = fwd()
+        torch.cuda.synchronize(dev)
+
+    def __call__(self, tokens: torch.Tensor, pos: torch.Tensor, slots: torch.Tensor,
+                 context_lens: torch.Tensor) -> torch.Tensor:
+        self.tokens.copy_(tokens)
+        self.pos.copy_(pos)
+        self.slots.copy_(slots)
+        self.lens.copy_(context_lens)
+        self.graph.replay()
+        return self.out
 
 
 class PagedKV:
@@ -202,7 +257,8 @@ class StepTimes:
 
 def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len: int = 128, block_size: int = 16,
         device: str | torch.device = "cuda", seed: int = 0, per_row: bool = False,
-        fused_decode: bool = False, capture_steps=(), fused_head: bool = False) -> tuple[StepTimes, list[list[int]]]:
+        fused_decode: bool = False, capture_steps=(), fused_head: bool = False,
+        graph: bool = False) -> tuple[StepTimes, list[list[int]]]:
     """Prefill every prompt, then decode in lockstep until each request has ``output_len``
     tokens. Half the requests are greedy, half top-k=50 / top-p=0.9 at temperature 1.0; the
     unseeded ones share one engine generator (engine.py:58). The batched path samples with
@@ -215,7 +271,11 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
     model.py:283): greedy rows take its tokens, the stochastic rows are sampled from the
     logits it writes (``rows=``), and a step with no stochastic row writes no logits. The
     forward time then ends at the final hidden state and the sampling time includes the
-    head. Returns the time split and the generated tokens."""
+    head. ``graph`` (with ``fused_decode``) replays the decode steps' forward from a HIP
+    graph (``DecodeGraph``) instead of launching it op by op; sampling stays eager. Returns
+    the time split and the generated tokens."""
+    if graph and not fused_decode:
+        raise ValueError("graph replays the fused decode step: pass fused_decode=True")
     device = torch.device(device)
     model = Model(shape, device, seed=seed)
     cache = PagedKV(shape, num_seqs, prompt_len + output_len, block_size, device, torch.bfloat16)
@@ -230,16 +290,23 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
     out: list[list[int]] = [[] for _ in range(num_seqs)]
     times = StepTimes(tokens_per_step=num_seqs)
     capture_steps = set(capture_steps)
+    dgraph = DecodeGraph(model, cache, num_seqs, prompt_len + output_len, hidden_only=fused_head) if graph else None
 
     def step(idx: int, tokens: torch.Tensor, start: int, q_len: int) -> list[int]:
         pos = torch.arange(start, start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
         slots = cache.slots(seq.view(-1, 1), pos).reshape(-1)
-        ctx = torch.arange(start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
-        seq_slots = cache.slots(seq.view(-1, 1), ctx)
-        torch.cuda.synchronize(device)
-        t0 = time.perf_counter()
-        out_f = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache, fused_decode,
-                              hidden_only=fused_head)
+        if dgraph is not None and q_len == 1:
+            lens = torch.full((num_seqs,), start + 1, dtype=torch.int32, device=device)
+            torch.cuda.synchronize(device)
+            t0 = time.perf_counter()
+            out_f = dgraph(tokens.reshape(-1), pos.reshape(-1), slots, lens)
+        else:
+            ctx = torch.arange(start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
+            seq_slots = cache.slots(seq.view(-1, 1), ctx)
+            torch.cuda.synchronize(device)
+            t0 = time.perf_counter()
+            out_f = model.forward(tokens.reshape(-1), pos.reshape(-1), slots, seq_slots, q_len, cache, fused_decode,
+                                  hidden_only=fused_head)
         torch.cuda.synchronize(device)
         t1 = time.perf_counter()
         if fused_head:

@@ -76,3 +76,27 @@ def test_greedy_rows_take_the_argmax(dev):
     from pagedbatch_amd import SamplingParams, sample
     toks = sample(logits, [SamplingParams(temperature=0.0)] * B, [torch.Generator()] * B)
     assert toks == [int(t) for t in torch.argmax(logits, dim=-1).cpu()]
+
+
+@pytest.mark.parametrize("fused_head", [False, True])
+def test_graph_replay_equals_eager_decode(dev, fused_head):
+    """The decode forward replayed from a HIP graph (engine_step.DecodeGraph) runs the same
+    kernels as the eager step: every step's logits (captured after each replay, with the
+    eager sampling, stop check and input preparation between replays) are bit-identical to
+    the eager run's, and so are the tokens and finish reasons."""
+    print(f"[case] engine step graph replay vs eager, fused_head={fused_head}", flush=True)
+    steps = 6
+    # head_dim 64 (the paged-attention kernel's), three layers, 2 query heads per KV head
+    shape = es.ModelShape(vocab_size=1000, hidden_size=256, intermediate_size=512, num_layers=3, num_heads=4,
+                          num_kv_heads=2)
+    kw = dict(num_seqs=8, prompt_len=16, output_len=steps, block_size=4, device=dev, fused_decode=True,
+              fused_head=fused_head)
+    if not fused_head:
+        kw["capture_steps"] = range(steps)
+    te, out_e = es.run(shape, **kw)
+    tg, out_g = es.run(shape, **kw, graph=True)
+    assert out_g == out_e
+    assert tg.reasons == te.reasons
+    for ce, cg in zip(te.captures, tg.captures):
+        assert ce.step == cg.step
+        assert torch.equal(ce.logits.view(torch.int16), cg.logits.view(torch.int16)), f"step {ce.step}"
