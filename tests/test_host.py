@@ -377,3 +377,24 @@ def test_decode_attention_rejects_bad_operands(kw, msg):
     t = _attn_tensors(**kw)
     with pytest.raises(ValueError, match=msg):
         decode_attention(t["q"], t["k"], t["v"], t["bt"], t["lens"], block_size=16, max_context=64)
+
+
+# ---------------------------------------------------------------- engine harness (host side)
+def test_engine_graph_needs_the_fused_decode_step():
+    from pagedbatch_amd import engine_step as es
+
+    with pytest.raises(ValueError, match="fused_decode"):
+        es.run(es.ModelShape.tiny(), num_seqs=2, prompt_len=4, output_len=2, block_size=4, device="cpu", graph=True)
+
+
+def test_engine_forward_without_seq_slots_needs_context_lens():
+    import torch
+
+    from pagedbatch_amd import engine_step as es
+
+    shape = es.ModelShape.tiny()
+    model = es.Model(shape, torch.device("cpu"))
+    cache = es.PagedKV(shape, 2, 8, 4, "cpu", torch.bfloat16)
+    t = torch.zeros(2, dtype=torch.long)
+    with pytest.raises(ValueError, match="context_lens"):
+        model.forward(t, t, t, None, 1, cache, fused_decode=True)
