@@ -34,10 +34,10 @@ extern "C" {
  *   v_cache       same layout as k_cache
  *   block_table   device int32[rows][max_blocks]
  *   context_lens  device int32[rows], each in [1, max_context]
- *   max_context   host bound on every context_lens[b] (sizes the kernel's LDS)
+ *   max_context   host bound on every context_lens[b]
  *   out           device float[rows][n_heads][head_dim]
- * head_dim must be 64, n_heads a multiple of n_kv_heads with at most 8 query heads per
- * KV head, max_context <= 2048 (EngineConfig.max_model_len's default), n_slots < 2^31; q,
+ * head_dim must be 64 or 128, n_heads a multiple of n_kv_heads with at most 8 query heads
+ * per KV head, max_context <= 2^20, n_slots < 2^31; q,
  * k_cache and v_cache 16-byte aligned. A slot outside [0, n_slots) (a corrupt block table)
  * makes that sequence's output NaN instead of reading out of bounds. Returns 0 or a
  * negative PBS_ERR_* code (pbs_last_error() says why); asynchronous on `stream`.

@@ -17,7 +17,7 @@ from . import _lib
 from .sampling import SamplerError
 
 
-HEAD_DIM = 64  # the only head size the kernel serves (k_decode indexes [slot][kv_head][64])
+HEAD_DIMS = (64, 128)  # the head sizes the kernel serves (k_decode indexes [slot][kv_head][head_dim])
 
 
 def _check_args(q, k_cache, v_cache, block_table, context_lens) -> None:
@@ -28,8 +28,8 @@ def _check_args(q, k_cache, v_cache, block_table, context_lens) -> None:
     if q.dtype != torch.float32 or q.dim() != 3 or not q.is_contiguous():
         raise ValueError("q must be a contiguous fp32 [rows, n_heads, head_dim] tensor")
     rows, n_heads, head_dim = q.shape
-    if head_dim != HEAD_DIM:
-        raise ValueError(f"head_dim must be {HEAD_DIM}, got {head_dim}")
+    if head_dim not in HEAD_DIMS:
+        raise ValueError(f"head_dim must be 64 or 128, got {head_dim}")
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         if c.dtype != torch.bfloat16 or c.dim() != 3 or not c.is_contiguous():
             raise ValueError(f"{name} must be a contiguous bf16 [n_slots, n_kv_heads, head_dim] tensor")
@@ -57,9 +57,10 @@ def _check_args(q, k_cache, v_cache, block_table, context_lens) -> None:
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
                      context_lens: torch.Tensor, block_size: int, max_context: int,
                      scale: float | None = None) -> torch.Tensor:
-    """q: fp32 [rows, n_heads, 64]; k_cache / v_cache: bf16 [n_slots, n_kv_heads, 64];
+    """q: fp32 [rows, n_heads, head_dim] (head_dim 64 or 128); k_cache / v_cache: bf16
+    [n_slots, n_kv_heads, head_dim];
     block_table: int32 [rows, max_blocks]; context_lens: int32 [rows], each in
-    [1, max_context]. Returns fp32 [rows, n_heads, 64]. Asynchronous on the current
+    [1, max_context]. Returns fp32 [rows, n_heads, head_dim]. Asynchronous on the current
     stream; a sequence whose block table points outside the pools gets NaN."""
     _check_args(q, k_cache, v_cache, block_table, context_lens)
     rows, n_heads, head_dim = q.shape

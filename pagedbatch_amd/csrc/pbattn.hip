@@ -30,9 +30,8 @@ namespace pba {
 
 constexpr int NT = 256;
 constexpr int NW = NT / 64;  // waves per workgroup
-constexpr int D = 64;
 constexpr int MAX_REP = 8;
-constexpr int MAX_CONTEXT = 2048;
+constexpr int MAX_CONTEXT = 1 << 20;  // positions stay below 2^22 (the block-index split)
 constexpr int QUAD_XOR1 = 0xb1, QUAD_XOR2 = 0x4e, ROW_HALF_MIRROR = 0x141;
 
 struct Args {
@@ -76,32 +75,40 @@ __device__ __forceinline__ float groups_sum(float v) {
   return v;
 }
 
-template <int REP>
+// DH: the head size (64 or 128); each lane holds DPL = DH / 8 dims of NJ positions, so a
+// chunk is 8 NJ positions and a lane's K and V pieces stay at 128 bytes each (64 for more
+// than four query heads of 128, whose query and accumulator registers leave less room)
+template <int REP, int DH>
 __global__ __launch_bounds__(NT) void k_decode(Args a) {
-  __shared__ float m_s[NW][MAX_REP], s_s[NW][MAX_REP];
-  __shared__ float acc_s[NW][MAX_REP][D];
+  constexpr int DPL = DH / 8;                          // dims per lane
+  constexpr int NJ = DH == 64 ? 8 : (REP > 4 ? 2 : 4);  // positions per lane and chunk
+  constexpr int CH = 8 * NJ;       // positions per chunk
+  constexpr int NQ = DPL / 8;      // 16-byte pieces per lane and row
+  __shared__ float m_s[NW][REP], s_s[NW][REP];
+  __shared__ float acc_s[NW][REP][DH];
   __shared__ int bad_s[NW];
 
   const int b = blockIdx.x / a.n_kv_heads;
   const int kvh = blockIdx.x % a.n_kv_heads;
   const int L = a.context_lens[b];
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
-  const int g = l >> 3, e0 = 8 * (l & 7);
-  float* out = a.out + ((size_t)b * a.n_heads + (size_t)kvh * REP) * D;
+  const int g = l >> 3, e0 = DPL * (l & 7);
+  float* out = a.out + ((size_t)b * a.n_heads + (size_t)kvh * REP) * DH;
   if (L < 1 || L > a.max_context) {  // out of the declared range: no reads, NaN out
-    for (int i = tid; i < REP * D; i += NT) out[i] = __int_as_float(0x7fc00000);
+    for (int i = tid; i < REP * DH; i += NT) out[i] = __int_as_float(0x7fc00000);
     return;
   }
-  // the lane's 8 dims of every query head of the group
-  float qv[REP][8];
+  // the lane's DPL dims of every query head of the group
+  float qv[REP][DPL];
   {
-    const float4* qp = (const float4*)(a.q + ((size_t)b * a.n_heads + (size_t)kvh * REP) * D + e0);
+    const float4* qp = (const float4*)(a.q + ((size_t)b * a.n_heads + (size_t)kvh * REP) * DH + e0);
 #pragma unroll
-    for (int h = 0; h < REP; ++h) {
-      const float4 x0 = qp[h * (D / 4)], x1 = qp[h * (D / 4) + 1];
-      qv[h][0] = x0.x, qv[h][1] = x0.y, qv[h][2] = x0.z, qv[h][3] = x0.w;
-      qv[h][4] = x1.x, qv[h][5] = x1.y, qv[h][6] = x1.z, qv[h][7] = x1.w;
-    }
+    for (int h = 0; h < REP; ++h)
+#pragma unroll
+      for (int i = 0; i < DPL / 4; ++i) {
+        const float4 x = qp[h * (DH / 4) + i];
+        qv[h][4 * i] = x.x, qv[h][4 * i + 1] = x.y, qv[h][4 * i + 2] = x.z, qv[h][4 * i + 3] = x.w;
+      }
   }
   // position p -> (block index, offset): (p + 0.5) * fl(1 / block_size) is within
   // (p + 0.5) * 2^-23 of the exact quotient, below its 0.5 / block_size distance from an
@@ -109,21 +116,21 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
   const float inv_bs = 1.0f / (float)a.block_size;
   const int32_t* bt = a.block_table + (size_t)b * a.max_blocks;
 
-  float m_run[REP], s_run[REP], acc[REP][8];
+  float m_run[REP], s_run[REP], acc[REP][DPL];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
     m_run[h] = -__builtin_inff();
     s_run[h] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+    for (int e = 0; e < DPL; ++e) acc[h][e] = 0.0f;
   }
   int bad = 0;
-  for (int t0 = 64 * w; t0 < L; t0 += 64 * NW) {
+  for (int t0 = CH * w; t0 < L; t0 += CH * NW) {
     // slots of the lane's positions t0 + 8 j + g (positions past the context read slot 0,
     // a bad block-table entry reads slot 0 and marks the sequence)
-    int64_t row[8];
+    int64_t row[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int pos = t0 + 8 * j + g;
       const int bi = (int)(((float)pos + 0.5f) * inv_bs);
       const int32_t blk = pos < L ? bt[bi] : 0;
@@ -132,23 +139,33 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
       bad |= (pos < L && !ok) ? 1 : 0;
       row[j] = ((ok && pos < L) ? slot : 0) * a.n_kv_heads + kvh;
     }
-    uint4 kq[8], vq[8];
+    uint4 kq[NJ][NQ], vq[NJ][NQ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kq[j] = *(const uint4*)(a.k + row[j] * D + e0);
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) vq[j] = *(const uint4*)(a.v + row[j] * D + e0);
+      for (int i = 0; i < NQ; ++i) kq[j][i] = *(const uint4*)(a.k + row[j] * DH + e0 + 8 * i);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) vq[j][i] = *(const uint4*)(a.v + row[j] * DH + e0 + 8 * i);
 
-    // scores of the lane's 8 positions for every head (-inf past the context)
-    float sc[REP][8];
+    // scores of the lane's NJ positions for every head (-inf past the context)
+    float sc[REP][NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float kv[8] = {bf16_lo(kq[j].x), bf16_hi(kq[j].x), bf16_lo(kq[j].y), bf16_hi(kq[j].y),
-                           bf16_lo(kq[j].z), bf16_hi(kq[j].z), bf16_lo(kq[j].w), bf16_hi(kq[j].w)};
+    for (int j = 0; j < NJ; ++j) {
+      float kv[DPL];
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        kv[8 * i] = bf16_lo(kq[j][i].x), kv[8 * i + 1] = bf16_hi(kq[j][i].x);
+        kv[8 * i + 2] = bf16_lo(kq[j][i].y), kv[8 * i + 3] = bf16_hi(kq[j][i].y);
+        kv[8 * i + 4] = bf16_lo(kq[j][i].z), kv[8 * i + 5] = bf16_hi(kq[j][i].z);
+        kv[8 * i + 6] = bf16_lo(kq[j][i].w), kv[8 * i + 7] = bf16_hi(kq[j][i].w);
+      }
 #pragma unroll
       for (int h = 0; h < REP; ++h) {
         float d = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qv[h][e], kv[e], d);
+        for (int e = 0; e < DPL; ++e) d = fmaf(qv[h][e], kv[e], d);
         d = group8_sum(d) * a.scale;
         sc[h][j] = (t0 + 8 * j + g < L) ? d : -__builtin_inff();
       }
@@ -158,27 +175,30 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
     for (int h = 0; h < REP; ++h) {
       float mc = sc[h][0];
 #pragma unroll
-      for (int j = 1; j < 8; ++j) mc = fmaxf(mc, sc[h][j]);
+      for (int j = 1; j < NJ; ++j) mc = fmaxf(mc, sc[h][j]);
       mc = groups_max(mc);
       const float mn = fmaxf(m_run[h], mc);  // finite: the chunk holds a position < L
       const float alpha = __expf(m_run[h] - mn);
       m_run[h] = mn;
       float ps = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+      for (int e = 0; e < DPL; ++e) acc[h][e] *= alpha;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const float pj = __expf(sc[h][j] - mn);
         ps += pj;
-        const uint4 vw = vq[j];
-        acc[h][0] = fmaf(pj, bf16_lo(vw.x), acc[h][0]);
-        acc[h][1] = fmaf(pj, bf16_hi(vw.x), acc[h][1]);
-        acc[h][2] = fmaf(pj, bf16_lo(vw.y), acc[h][2]);
-        acc[h][3] = fmaf(pj, bf16_hi(vw.y), acc[h][3]);
-        acc[h][4] = fmaf(pj, bf16_lo(vw.z), acc[h][4]);
-        acc[h][5] = fmaf(pj, bf16_hi(vw.z), acc[h][5]);
-        acc[h][6] = fmaf(pj, bf16_lo(vw.w), acc[h][6]);
-        acc[h][7] = fmaf(pj, bf16_hi(vw.w), acc[h][7]);
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+          const uint4 vw = vq[j][i];
+          acc[h][8 * i] = fmaf(pj, bf16_lo(vw.x), acc[h][8 * i]);
+          acc[h][8 * i + 1] = fmaf(pj, bf16_hi(vw.x), acc[h][8 * i + 1]);
+          acc[h][8 * i + 2] = fmaf(pj, bf16_lo(vw.y), acc[h][8 * i + 2]);
+          acc[h][8 * i + 3] = fmaf(pj, bf16_hi(vw.y), acc[h][8 * i + 3]);
+          acc[h][8 * i + 4] = fmaf(pj, bf16_lo(vw.z), acc[h][8 * i + 4]);
+          acc[h][8 * i + 5] = fmaf(pj, bf16_hi(vw.z), acc[h][8 * i + 5]);
+          acc[h][8 * i + 6] = fmaf(pj, bf16_lo(vw.w), acc[h][8 * i + 6]);
+          acc[h][8 * i + 7] = fmaf(pj, bf16_hi(vw.w), acc[h][8 * i + 7]);
+        }
       }
       s_run[h] = s_run[h] * alpha + ps;
     }
@@ -189,14 +209,14 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
   for (int h = 0; h < REP; ++h) {
     s_run[h] = groups_sum(s_run[h]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = groups_sum(acc[h][e]);
+    for (int e = 0; e < DPL; ++e) acc[h][e] = groups_sum(acc[h][e]);
   }
   const bool wave_bad = __any(bad);
   if (l < 8) {
 #pragma unroll
     for (int h = 0; h < REP; ++h) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc_s[w][h][e0 + e] = acc[h][e];
+      for (int e = 0; e < DPL; ++e) acc_s[w][h][e0 + e] = acc[h][e];
       if (l == 0) {
         m_s[w][h] = m_run[h];
         s_s[w][h] = s_run[h];
@@ -208,8 +228,8 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
   bool any_bad = false;
 #pragma unroll
   for (int ww = 0; ww < NW; ++ww) any_bad |= bad_s[ww] != 0;
-  for (int i = tid; i < REP * D; i += NT) {
-    const int h = i / D, d = i % D;
+  for (int i = tid; i < REP * DH; i += NT) {
+    const int h = i / DH, d = i % DH;
     if (any_bad) {  // a corrupt slot anywhere in the context: NaN out
       out[i] = __int_as_float(0x7fc00000);
       continue;
@@ -228,6 +248,20 @@ __global__ __launch_bounds__(NT) void k_decode(Args a) {
   }
 }
 
+template <int DH>
+void launch_decode(const Args& a, dim3 grid, hipStream_t st) {
+  switch (a.rep) {
+    case 1: hipLaunchKernelGGL((k_decode<1, DH>), grid, dim3(NT), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((k_decode<2, DH>), grid, dim3(NT), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((k_decode<3, DH>), grid, dim3(NT), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((k_decode<4, DH>), grid, dim3(NT), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((k_decode<5, DH>), grid, dim3(NT), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((k_decode<6, DH>), grid, dim3(NT), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((k_decode<7, DH>), grid, dim3(NT), 0, st, a); break;
+    default: hipLaunchKernelGGL((k_decode<8, DH>), grid, dim3(NT), 0, st, a); break;
+  }
+}
+
 }  // namespace pba
 
 extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int64_t n_slots,
@@ -239,7 +273,8 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
   if (rows == 0) return PBS_OK;
   if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out)
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "null device pointer");
-  if (head_dim != D) return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "head_dim must be 64");
+  if (head_dim != 64 && head_dim != 128)
+    return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "head_dim must be 64 or 128");
   if (n_kv_heads < 1 || n_heads < n_kv_heads || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > MAX_REP)
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT,
                              "n_heads must be a multiple of n_kv_heads, at most 8 query heads per KV head");
@@ -247,7 +282,7 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "block_size, max_blocks and n_slots must be positive");
   if (max_context < 1 || max_context > MAX_CONTEXT || (int64_t)max_context > max_blocks * block_size)
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT,
-                             "max_context must be in [1, 2048] and covered by max_blocks * block_size");
+                             "max_context must be in [1, 1048576] and covered by max_blocks * block_size");
   if (rows * n_kv_heads > 0x7fffffff) return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "too many rows");
   if (n_slots > 0x7fffffff)
     return pbs::report_error(PBS_ERR_INVALID_ARGUMENT, "n_slots must be below 2^31");
@@ -268,18 +303,9 @@ extern "C" int pba_decode_attention(const float* q, const uint16_t* k_cache, con
   a.max_context = max_context;
   a.scale = scale;
   a.out = out;
-  const dim3 grid((unsigned)(rows * n_kv_heads)), block(NT);
-  hipStream_t st = (hipStream_t)stream;
-  switch (a.rep) {
-    case 1: hipLaunchKernelGGL(k_decode<1>, grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_decode<2>, grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL(k_decode<3>, grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL(k_decode<4>, grid, block, 0, st, a); break;
-    case 5: hipLaunchKernelGGL(k_decode<5>, grid, block, 0, st, a); break;
-    case 6: hipLaunchKernelGGL(k_decode<6>, grid, block, 0, st, a); break;
-    case 7: hipLaunchKernelGGL(k_decode<7>, grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL(k_decode<8>, grid, block, 0, st, a); break;
-  }
+  const dim3 grid((unsigned)(rows * n_kv_heads));
+  if (head_dim == 64) launch_decode<64>(a, grid, (hipStream_t)stream);
+  else launch_decode<128>(a, grid, (hipStream_t)stream);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return pbs::report_error(PBS_ERR_HIP, hipGetErrorString(e));
   return PBS_OK;

@@ -30,14 +30,19 @@ def _torch_decode(q, kc, vc, block_table, lens, block_size, scale):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed", [(4, 9, 3, 16, 200, 1), (3, 8, 8, 8, 37, 2), (2, 16, 2, 32, 1500, 3),
-                                                   (5, 4, 1, 16, 1, 4), (2, 16, 2, 16, 2048, 5)])
-def test_decode_matches_torch(B, Hq, Hkv, bs, maxL, seed):
+@pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed,D", [
+    (4, 9, 3, 16, 200, 1, 64), (3, 8, 8, 8, 37, 2, 64), (2, 16, 2, 32, 1500, 3, 64), (5, 4, 1, 16, 1, 4, 64),
+    (2, 16, 2, 16, 2048, 5, 64),
+    (2, 9, 3, 16, 5000, 6, 64),      # a context past 2048
+    (3, 32, 8, 16, 700, 7, 128),     # head_dim 128, four query heads per KV head (a Llama-3-8B layer)
+    (2, 64, 8, 16, 300, 8, 128),     # eight per KV head (a Llama-3-70B layer)
+    (3, 6, 1, 8, 90, 9, 128),        # six per KV head
+])
+def test_decode_matches_torch(B, Hq, Hkv, bs, maxL, seed, D):
     from pagedbatch_amd.attention import decode_attention
 
-    print(f"[case] decode B={B} Hq={Hq} Hkv={Hkv} bs={bs} maxL={maxL}", flush=True)
+    print(f"[case] decode B={B} Hq={Hq} Hkv={Hkv} bs={bs} maxL={maxL} D={D}", flush=True)
     g = torch.Generator().manual_seed(seed)
-    D = 64
     nblk = (maxL + bs - 1) // bs
     n_slots = B * nblk * bs + 3 * bs
     kc = (torch.randn(n_slots, Hkv, D, generator=g) * 0.5).to(torch.bfloat16)
@@ -54,8 +59,9 @@ def test_decode_matches_torch(B, Hq, Hkv, bs, maxL, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed", [(4, 9, 3, 16, 200, 11), (3, 8, 2, 16, 700, 12), (2, 4, 4, 8, 1, 13)])
-def test_decode_matches_reference_bf16_sdpa(B, Hq, Hkv, bs, maxL, seed):
+@pytest.mark.parametrize("B,Hq,Hkv,bs,maxL,seed,D", [(4, 9, 3, 16, 200, 11, 64), (3, 8, 2, 16, 700, 12, 64),
+                                                     (2, 4, 4, 8, 1, 13, 64), (2, 32, 8, 16, 400, 14, 128)])
+def test_decode_matches_reference_bf16_sdpa(B, Hq, Hkv, bs, maxL, seed, D):
     """Against the reference's own arithmetic (model.py:212-222): bf16 q, K and V gathered
     through the slot table, the KV heads repeated, F.scaled_dot_product_attention in bf16
     (on the CPU). The kernel computes in fp32 from the same bf16 inputs; torch's bf16 result
@@ -65,9 +71,8 @@ def test_decode_matches_reference_bf16_sdpa(B, Hq, Hkv, bs, maxL, seed):
 
     from pagedbatch_amd.attention import decode_attention
 
-    print(f"[case] decode vs bf16 sdpa B={B} Hq={Hq} Hkv={Hkv} bs={bs} maxL={maxL}", flush=True)
+    print(f"[case] decode vs bf16 sdpa B={B} Hq={Hq} Hkv={Hkv} bs={bs} maxL={maxL} D={D}", flush=True)
     g = torch.Generator().manual_seed(seed)
-    D = 64
     nblk = (maxL + bs - 1) // bs
     n_slots = B * nblk * bs + bs
     kc = (torch.randn(n_slots, Hkv, D, generator=g) * 0.5).to(torch.bfloat16)

@@ -327,11 +327,11 @@ def _attn(lib, **kw):
 @pytest.mark.parametrize("kw,msg", [
     ({"rows": -1}, "negative"),
     ({"q": None}, "null"),
-    ({"d": 128}, "head_dim"),
+    ({"d": 96}, "head_dim must be 64 or 128"),
     ({"hq": 10}, "multiple"),
     ({"hq": 27}, "at most 8"),
     ({"maxc": 65}, "max_context"),
-    ({"maxc": 5000, "max_blocks": 400}, "max_context"),
+    ({"maxc": (1 << 20) + 1, "max_blocks": 1 << 17}, "max_context"),
     ({"bs": 0}, "block_size"),
     ({"n_slots": 1 << 31}, "n_slots"),
     ({"q": (1 << 20) + 4}, "16-byte aligned"),
@@ -357,7 +357,7 @@ def _attn_tensors(**kw):
 
 
 @pytest.mark.parametrize("kw,msg", [
-    ({"q": torch.zeros(2, 9, 32)}, "head_dim must be 64"),
+    ({"q": torch.zeros(2, 9, 32)}, "head_dim must be 64 or 128"),
     ({"k": torch.zeros(64, 3, 32, dtype=torch.bfloat16), "v": torch.zeros(64, 3, 32, dtype=torch.bfloat16)},
      "head_dim 32 differs"),
     ({"v": torch.zeros(64, 3, 64)}, "v_cache must be a contiguous bf16"),
