@@ -115,6 +115,23 @@ def test_decode_corrupt_block_table_gives_nan_not_a_fault():
 
 
 @pytest.mark.gpu
+def test_decode_context_length_out_of_range_gives_nan():
+    """A context length of 0 or past max_context: that sequence's output is NaN (no read),
+    the others are computed."""
+    from pagedbatch_amd.attention import decode_attention
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(21)
+    kc = torch.randn(64, 2, 128, generator=g).to(torch.bfloat16).to(dev)
+    bt = torch.tensor([[0, 1], [2, 3], [1, 0]], dtype=torch.int32, device=dev)
+    lens = torch.tensor([0, 20, 33], dtype=torch.int32, device=dev)  # max_context 32
+    q = torch.randn(3, 4, 128, generator=g).to(dev)
+    out = decode_attention(q, kc, kc, bt, lens, 16, 32).cpu()
+    assert torch.isnan(out[0]).all() and torch.isnan(out[2]).all()
+    assert torch.isfinite(out[1]).all()
+
+
+@pytest.mark.gpu
 def test_engine_decode_step_fused_matches_unfused():
     """One decode step of the tiny engine model on the same cache, attention fused or not:
     the same logits up to the bf16 rounding of the attention output (model.py:224's
