@@ -3086,6 +3086,7 @@ __global__ __launch_bounds__(NT_AM) void k_argmax(KArgs a) {
   constexpr size_t ELT = DTraits<DT>::B16 ? 2 : 4;
   __shared__ float red_v[NT_AM / 64];
   __shared__ int red_i[NT_AM / 64];
+  __shared__ int red_nan[NT_AM / 64];
   const int b = blockIdx.x;
   const int t = threadIdx.x;
   const int64_t lrow = a.row_map ? (int64_t)a.row_map[b] : (int64_t)b;
@@ -3151,8 +3152,25 @@ __global__ __launch_bounds__(NT_AM) void k_argmax(KArgs a) {
       bi = up ? i : bi;
     }
   }
-  // a row holding a NaN: its first NaN, found by a second pass
-  if (__syncthreads_or(nan)) {
+  // block reduction: the largest value, lowest index on ties; the NaN flags ride the same
+  // barrier
+  const int w = t >> 6;
+  {
+    const float wm = wmax_f32(bv);
+    const int wi = wmin_i32(bv == wm ? bi : INT32_MAX);
+    const bool wnan = __any(nan);
+    if ((t & 63) == 0) {
+      red_v[w] = wm;
+      red_i[w] = wi;
+      red_nan[w] = wnan ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  bool any_nan = false;
+#pragma unroll
+  for (int k = 0; k < NT_AM / 64; ++k) any_nan |= red_nan[k] != 0;
+  if (any_nan) {
+    // a row holding a NaN: its first NaN, found by a second pass, and the reduction again
     int ni = INT32_MAX;
     for (int i = t; i < a.vocab; i += NT_AM) {
       if (elem(i) != elem(i)) {
@@ -3162,16 +3180,15 @@ __global__ __launch_bounds__(NT_AM) void k_argmax(KArgs a) {
     }
     bv = ni != INT32_MAX ? INFINITY : -INFINITY;
     bi = ni;
+    const float wm = wmax_f32(bv);
+    const int wi = wmin_i32(bv == wm ? bi : INT32_MAX);
+    __syncthreads();  // every thread has read the flags before the table is rewritten
+    if ((t & 63) == 0) {
+      red_v[w] = wm;
+      red_i[w] = wi;
+    }
+    __syncthreads();
   }
-  // block reduction: the largest value, lowest index on ties
-  const float wm = wmax_f32(bv);
-  const int wi = wmin_i32(bv == wm ? bi : INT32_MAX);
-  const int w = t >> 6;
-  if ((t & 63) == 0) {
-    red_v[w] = wm;
-    red_i[w] = wi;
-  }
-  __syncthreads();
   if (t == 0) {
     float v = red_v[0];
     int i = red_i[0];
