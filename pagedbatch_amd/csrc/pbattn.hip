@@ -63,16 +63,25 @@ __device__ __forceinline__ float group8_sum(float v) {
   return v + dpp_f<ROW_HALF_MIRROR>(v);
 }
 
-// across the 8 groups of a wave (lanes l, l ^ 8, ..., l ^ 56)
+// across the 8 groups of a wave (lanes l, l ^ 8, ..., l ^ 56), without LDS: a DPP rotate by
+// 8 inside each 16-lane row pairs l with l ^ 8. v_permlane16_swap (v_permlane32_swap) of a
+// value with itself returns two registers that hold, in every lane, its own value and the
+// value of lane l ^ 16 (l ^ 32) in the same order for both lanes of a pair, so combining
+// the two gives both lanes the same result.
+constexpr int ROW_ROR8 = 0x128;
 __device__ __forceinline__ float groups_max(float v) {
-#pragma unroll
-  for (int off = 8; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, dpp_f<ROW_ROR8>(v));
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
 }
 __device__ __forceinline__ float groups_sum(float v) {
-#pragma unroll
-  for (int off = 8; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_f<ROW_ROR8>(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
 }
 
 // DH: the head size (64 or 128); each lane holds DPL = DH / 8 dims of NJ positions, so a
