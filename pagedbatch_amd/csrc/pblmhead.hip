@@ -63,6 +63,7 @@ struct Args {
   unsigned long long* part;  // [rows][tiles]: each (row, tile)'s largest (value, first column) key
   int64_t hstride;              // elements between hidden rows
   int rows, hdim, vocab;
+  int kslice;                   // k_lmhead_lds: hidden elements per LDS-resident slice (divides hdim)
 };
 
 // bf16 of an fp32 value: round to nearest, ties to even; NaN stays a (quiet) NaN
@@ -297,10 +298,11 @@ __global__ __launch_bounds__(64) void k_lmhead(Args a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// hidden_dim <= 1024: three waves per workgroup (192 columns) share the 64-row hidden block
-// in LDS, so the hidden fragments come from LDS (their own counter) and the memory
-// counter tracks weight loads only: each wait before a multiply covers exactly the weight
-// chunk it needs, with the later chunks still in flight.
+// Three waves per workgroup (192 columns) share the 64-row hidden block in LDS: the whole
+// hidden dimension up to 1024, or larger ones in equal slices of at most 1024 staged one
+// after the other (the accumulators carry over). The hidden fragments come from LDS
+// (their own counter), so the memory counter tracks weight loads only: each wait before
+// a multiply covers exactly the weight chunk it needs, with the later chunks in flight.
 // ---------------------------------------------------------------------------------------
 constexpr int LW_WAVES = 3;
 constexpr int LDS_HMAX = 1024;  // largest hidden_dim of this kernel
@@ -379,7 +381,8 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
   // the hidden block while the waves multiply, then (after a barrier) the waves' fp32
   // tiles over it
   extern __shared__ __align__(16) uint16_t smem[];
-  const int hs = a.hdim + 8;  // LDS row stride of the hidden block (the pad spreads the banks)
+  const int ks = a.kslice;    // hidden elements per slice: hidden_dim in one or more slices
+  const int hs = ks + 8;      // LDS row stride of the hidden block (the pad spreads the banks)
   uint16_t* hb = smem;        // [TM][hs]
   const int tid = threadIdx.x, l = tid & 63, wv = tid >> 6;
   float* tile = (float*)smem + wv * TM * TST;
@@ -392,10 +395,11 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
       (void*)a.weight, (short)0, (int)((int64_t)a.vocab * a.hdim * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a.hidden, (short)0, (int)((int64_t)a.rows * a.hstride * 2), 0x00020000);
-  const int nk = a.hdim / KC;
-  uint32_t woff[2];
+  const int nk = ks / KC;  // chunks per slice
+  const int nsl = a.hdim / ks;
+  uint32_t woff0[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) woff[t] = (uint32_t)((((int64_t)(n0 + 32 * t + r32)) * a.hdim + 32 * half) * 2);
+  for (int t = 0; t < 2; ++t) woff0[t] = (uint32_t)((((int64_t)(n0 + 32 * t + r32)) * a.hdim + 32 * half) * 2);
 
   for (int m0 = 0; m0 < a.rows; m0 += TM) {
     FragsW<D> f;
@@ -403,60 +407,70 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) f.acc[i][j] = (f32x16){};
-    // The hidden block (64 rows, zeros past the last, x hidden_dim; 16 bytes per piece) in
-    // batches of up to 24 pieces per thread in flight. The first weight chunks go out right
-    // behind the last batch, unconditionally (chunks past the row's end or past the
-    // buffer's end read harmless data or zeros, never used), so the wait before that
-    // batch's LDS writes leaves them in flight and the two latencies overlap.
-    const int per_row = a.hdim / 8;
-    const int npiece = TM * per_row;
-    constexpr int SB = 24, SSTEP = 64 * LW_WAVES;
-    // piece q -> (row q / per_row, column piece): ((q + 0.5) * fl(1 / per_row)) is within
-    // 2e-3 of (q + 0.5) / per_row for q < 2^14, and that quotient is at least
-    // 0.5 / per_row >= 1 / 256 from an integer, so the truncation is exact
-    const float inv_pr = 1.0f / (float)per_row;
-    const int nbatch = (npiece - tid + SB * SSTEP - 1) / (SB * SSTEP);  // >= 1: npiece >= 512 > tid
-    auto batch_loads = [&](int q0, u4 (&v)[SB]) {
+    // the slices of the hidden dimension, each staged like a whole block; the
+    // accumulators carry over, and the barrier after each slice's multiplies frees the
+    // LDS block for the next slice (or, after the last, for the tiles)
+#pragma unroll 1
+    for (int sl = 0; sl < nsl; ++sl) {
+      const int k0 = sl * ks;  // the slice's first hidden element
+      uint32_t woff[2];
 #pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const int q = min(q0 + u * SSTEP, npiece - 1);
-        const int r = (int)(((float)q + 0.5f) * inv_pr), c = q - r * per_row;
-        v[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          hrs, (uint32_t)((((int64_t)(m0 + r)) * a.hstride + 8 * c) * 2), 0, 0));
+      for (int t = 0; t < 2; ++t) woff[t] = woff0[t] + (uint32_t)(k0 * 2);
+      // The hidden block (64 rows, zeros past the last, x hidden_dim; 16 bytes per piece) in
+      // batches of up to 24 pieces per thread in flight. The first weight chunks go out right
+      // behind the last batch, unconditionally (chunks past the row's end or past the
+      // buffer's end read harmless data or zeros, never used), so the wait before that
+      // batch's LDS writes leaves them in flight and the two latencies overlap.
+      const int per_row = ks / 8;
+      const int npiece = TM * per_row;
+      constexpr int SB = 24, SSTEP = 64 * LW_WAVES;
+      // piece q -> (row q / per_row, column piece): ((q + 0.5) * fl(1 / per_row)) is within
+      // 2e-3 of (q + 0.5) / per_row for q < 2^14, and that quotient is at least
+      // 0.5 / per_row >= 1 / 256 from an integer, so the truncation is exact
+      const float inv_pr = 1.0f / (float)per_row;
+      const int nbatch = (npiece - tid + SB * SSTEP - 1) / (SB * SSTEP);  // >= 1: npiece >= 512 > tid
+      auto batch_loads = [&](int q0, u4 (&v)[SB]) {
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int q = min(q0 + u * SSTEP, npiece - 1);
+          const int r = (int)(((float)q + 0.5f) * inv_pr), c = q - r * per_row;
+          v[u] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            hrs, (uint32_t)((((int64_t)(m0 + r)) * a.hstride + k0 + 8 * c) * 2), 0, 0));
+        }
+      };
+      // (a clamped piece is the last one, loaded and stored again with the same value)
+      auto batch_stores = [&](int q0, const u4 (&v)[SB]) {
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int q = min(q0 + u * SSTEP, npiece - 1);
+          const int r = (int)(((float)q + 0.5f) * inv_pr), c = q - r * per_row;
+          *(u4*)(hb + r * hs + 8 * c) = v[u];
+        }
+      };
+      for (int b = 0; b + 1 < nbatch; ++b) {
+        u4 v[SB];
+        batch_loads(tid + b * SB * SSTEP, v);
+        batch_stores(tid + b * SB * SSTEP, v);
       }
-    };
-    // (a clamped piece is the last one, loaded and stored again with the same value)
-    auto batch_stores = [&](int q0, const u4 (&v)[SB]) {
+      {
+        const int q0 = tid + (nbatch - 1) * SB * SSTEP;
+        u4 v[SB];
+        batch_loads(q0, v);
 #pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const int q = min(q0 + u * SSTEP, npiece - 1);
-        const int r = (int)(((float)q + 0.5f) * inv_pr), c = q - r * per_row;
-        *(u4*)(hb + r * hs + 8 * c) = v[u];
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
+        batch_stores(q0, v);
       }
-    };
-    for (int b = 0; b + 1 < nbatch; ++b) {
-      u4 v[SB];
-      batch_loads(tid + b * SB * SSTEP, v);
-      batch_stores(tid + b * SB * SSTEP, v);
+      __syncthreads();
+      if (active) {
+        // whole groups of D chunks while another group follows them, then the last R
+        int kc0 = 0;
+        for (; kc0 + 2 * D <= nk; kc0 += D) kgroup_lds<D>(f, wrs, woff, hb, hs, r32, half, kc0);
+        ktail_lds<D, R>(f, wrs, woff, hb, hs, r32, half, kc0);
+      }
+      __syncthreads();  // every wave's hidden reads are done: the next slice or the tiles overwrite the block
     }
-    {
-      const int q0 = tid + (nbatch - 1) * SB * SSTEP;
-      u4 v[SB];
-      batch_loads(q0, v);
-#pragma unroll
-      for (int d = 0; d < D; ++d)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) load_frag(wrs, woff[t] + (uint32_t)(d * KC * 2), f.w[d][t]);
-      batch_stores(q0, v);
-    }
-    __syncthreads();
-    if (active) {
-      // whole groups of D chunks while another group follows them, then the last R
-      int kc0 = 0;
-      for (; kc0 + 2 * D <= nk; kc0 += D) kgroup_lds<D>(f, wrs, woff, hb, hs, r32, half, kc0);
-      ktail_lds<D, R>(f, wrs, woff, hb, hs, r32, half, kc0);
-    }
-    __syncthreads();  // every wave's hidden reads are done: the tiles overwrite the block
     if (active) epilogue(a, tile, f.acc, m0, n0, tile_id, ntiles, l, half, r32);
     __syncthreads();  // the tiles are read before the next row block's hidden block
   }
@@ -599,15 +613,25 @@ int pbs_lm_head_argmax(const uint16_t* hidden, int64_t hidden_stride, const uint
   a.hdim = (int)hidden_dim;
   a.vocab = (int)vocab;
   const unsigned ntiles = (unsigned)((vocab + pbl::TN - 1) / pbl::TN);
+  // the LDS-resident hidden block: hidden_dim whole, or in the fewest equal slices of at
+  // most LDS_HMAX elements (each a multiple of 64); otherwise the L2-fragment kernel
+  int kslice = 0;
   if (hidden_dim <= pbl::LDS_HMAX) {
-    const size_t lds = std::max(pbl::lds_hidden_bytes((int)hidden_dim), pbl::LDS_TILES);
+    kslice = (int)hidden_dim;
+  } else {
+    for (int n = 2; n <= 16 && !kslice; ++n)
+      if (hidden_dim % (pbl::KC * n) == 0 && hidden_dim / n <= pbl::LDS_HMAX) kslice = (int)(hidden_dim / n);
+  }
+  a.kslice = kslice;
+  if (kslice) {
+    const size_t lds = std::max(pbl::lds_hidden_bytes(kslice), pbl::LDS_TILES);
     if (lds > 64 * 1024) {
-      const int rc = lds_attribute((int)(hidden_dim / pbl::KC));
+      const int rc = lds_attribute(kslice / pbl::KC);
       if (rc != PBS_OK) return rc;
     }
     const dim3 grid((ntiles + pbl::LW_WAVES - 1) / pbl::LW_WAVES), block(64 * pbl::LW_WAVES);
     void* args[] = {&a};
-    const hipError_t el = hipLaunchKernel(pbl::lds_kernel((int)(hidden_dim / pbl::KC)), grid, block, args, lds,
+    const hipError_t el = hipLaunchKernel(pbl::lds_kernel(kslice / pbl::KC), grid, block, args, lds,
                                           (hipStream_t)stream);
     if (el != hipSuccess) return pbs::report_errorf(PBS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(el));
   } else {

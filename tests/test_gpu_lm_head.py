@@ -84,8 +84,10 @@ def check(dev, rows, hdim, vocab, seed, scale=1.0, plant=None):
     (3, 448, 129),      # 7 chunks: a last group of seven
     (17, 960, 1500),    # 15 chunks: two groups, then seven
     (70, 1024, 640),    # the largest LDS-resident hidden block, two row blocks
-    (8, 1088, 3000),    # hidden_dim past the LDS-resident limit: the L2-fragment kernel
-    (65, 2048, 700),
+    (8, 1088, 3000),    # 17 chunks: no equal slices of at most 1024, so the L2-fragment kernel
+    (65, 2048, 700),    # two LDS-resident slices of 1024
+    (33, 3072, 500),    # three slices of 1024
+    (9, 1280, 999),     # two slices of 640 (ten chunks each: a last group of six)
 ])
 def test_lm_head_matches_exact_dot_products(dev, rows, hdim, vocab):
     check(dev, rows, hdim, vocab, seed=rows * 7 + vocab)
