@@ -478,7 +478,7 @@ __global__ __launch_bounds__(64 * LW_WAVES) void k_lmhead_lds(Args a) {
 
 // the k_lmhead_lds instantiation for a row of nk chunks (1 <= nk <= LDS_HMAX / KC)
 template <int D, int... Rs>
-constexpr const void* lds_kernel_for(int r, std::integer_sequence<int, Rs...>) {
+const void* lds_kernel_for(int r, std::integer_sequence<int, Rs...>) {
   const void* k = nullptr;
   ((k = (r == D + Rs) ? (const void*)k_lmhead_lds<D, D + Rs> : k), ...);
   return k;
