@@ -8,8 +8,8 @@ per-row uniforms drawn from the caller's seeded generators, and the ctypes bindi
 """
 
 from .config import SamplingParams
-from .sampling import SamplerError, sample, sample_and_finish, sample_token
+from .sampling import SamplerError, SamplingGraph, sample, sample_and_finish, sample_token
 
 __version__ = "0.2.0"
 
-__all__ = ["SamplingParams", "SamplerError", "sample", "sample_and_finish", "sample_token"]
+__all__ = ["SamplingParams", "SamplerError", "SamplingGraph", "sample", "sample_and_finish", "sample_token"]

@@ -29,7 +29,7 @@ import torch.nn.functional as F
 from .attention import decode_attention
 from .config import SamplingParams
 from .finish import FinishRule
-from .sampling import _uniforms, sample_and_finish
+from .sampling import SamplingGraph, _uniforms, sample_and_finish
 
 
 @dataclass
@@ -272,8 +272,10 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
     logits it writes (``rows=``), and a step with no stochastic row writes no logits. The
     forward time then ends at the final hidden state and the sampling time includes the
     head. ``graph`` (with ``fused_decode``) replays the decode steps' forward from a HIP
-    graph (``DecodeGraph``) instead of launching it op by op; sampling stays eager. Returns
-    the time split and the generated tokens."""
+    graph (``DecodeGraph``) instead of launching it op by op, and (without ``fused_head``)
+    their sampling call from a second one (``sampling.SamplingGraph``): the host then only
+    draws the uniforms, writes the stop rules' counts and synchronises. Returns the time
+    split and the generated tokens."""
     if graph and not fused_decode:
         raise ValueError("graph replays the fused decode step: pass fused_decode=True")
     device = torch.device(device)
@@ -291,6 +293,13 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
     times = StepTimes(tokens_per_step=num_seqs)
     capture_steps = set(capture_steps)
     dgraph = DecodeGraph(model, cache, num_seqs, prompt_len + output_len, hidden_only=fused_head) if graph else None
+    # with the graph-replayed forward, the decode steps' sampling call is a graph too (on
+    # the decode graph's fixed logits buffer); the stop rules' counts change every step
+    sgraph = None
+    if dgraph is not None and not fused_head and not per_row:
+        rules0 = [FinishRule(ignore_eos=False, stop_token_ids=(), num_output=1, max_tokens=output_len,
+                             num_tokens=prompt_len + 1)] * num_seqs
+        sgraph = SamplingGraph(dgraph.out, params, finish_rules=rules0, max_model_len=prompt_len + output_len)
 
     def step(idx: int, tokens: torch.Tensor, start: int, q_len: int) -> list[int]:
         pos = torch.arange(start, start + q_len, device=device).view(1, -1).expand(num_seqs, -1)
@@ -333,7 +342,10 @@ def run(shape: ModelShape, num_seqs: int = 64, prompt_len: int = 128, output_len
             n_out = len(out[0]) + 1  # outputs after this token (lockstep)
             rules = [FinishRule(ignore_eos=False, stop_token_ids=(), num_output=n_out, max_tokens=output_len,
                                 num_tokens=prompt_len + n_out)] * num_seqs
-            toks, reasons = sample_and_finish(logits, params, gens, rules, None, prompt_len + output_len)
+            if sgraph is not None and q_len == 1:
+                toks, reasons = sgraph(gens, rules)
+            else:
+                toks, reasons = sample_and_finish(logits, params, gens, rules, None, prompt_len + output_len)
             times.reasons.append(reasons)
         t2 = time.perf_counter()
         times.forward_s.append(t1 - t0)

@@ -185,24 +185,14 @@ def _raise_for_status(status: np.ndarray, temperature: np.ndarray | None = None)
     raise RuntimeError(_BAD_PROBS)
 
 
-def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, finish=None, timing=None,
-            greedy: bool = False):
-    """Copy the staged params to the device and call the C ABI (``pbs_argmax`` when
-    ``greedy``: every row greedy with valid parameters); with ``finish`` (eos id,
-    max_model_len, number of stop ids) also the stop check, on the sampler's device tokens.
-    Returns host tokens, statuses and reasons (None without ``finish``) plus the device
-    diagnostics of a debug call."""
-    lib = _lib.load()
+def _args(logits, n: int, row_map_given: bool, bufs: _Buffers) -> list:
+    """The C ABI arguments shared by pbs_sample, pbs_sample_debug and (the first seven)
+    pbs_argmax: the logits, the staged per-row arrays on the device and the outputs."""
     cap = bufs.cap
-    stream = torch.cuda.current_stream(logits.device)
-    sp = stream.cuda_stream
-    words = bufs.fin if finish is None else bufs.stop_ids + finish[2]
-    bufs.d_in[:words].copy_(bufs.h_in[:words], non_blocking=True)
     base = bufs.d_in.data_ptr()
     ptr = [base + 4 * i * cap for i in range(5)]
     out_tok = bufs.d_out.data_ptr()
-    out_st = out_tok + 4 * cap
-    args = [
+    return [
         logits.data_ptr(),
         _TORCH_DTYPE[logits.dtype],
         logits.shape[0],
@@ -215,30 +205,42 @@ def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, fi
         ptr[_IN_P],
         ptr[_IN_U],
         out_tok,
-        out_st,
+        out_tok + 4 * cap,
     ]
-    probs = kept = info = None
-    if debug:
-        V = logits.shape[1]
-        probs = torch.empty((n, V), dtype=torch.float32, device=logits.device)
-        kept = torch.empty((n, V), dtype=torch.uint8, device=logits.device)
-        info = torch.empty(n * _lib.ROW_INFO_DTYPE.itemsize, dtype=torch.uint8, device=logits.device)
-        rc = lib.pbs_sample_debug(*args, probs.data_ptr(), kept.data_ptr(), info.data_ptr(), None, 0, sp)
-    elif greedy:
-        rc = lib.pbs_argmax(*args[:7], out_tok, out_st, sp)
+
+
+def _raise_for_rc(lib, rc: int, what: str) -> None:
+    if rc == _lib.OK:
+        return
+    msg = _lib.last_error(lib)
+    if rc == _lib.ERR_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    if rc == _lib.ERR_UNSUPPORTED_DTYPE:
+        raise TypeError(msg)
+    raise SamplerError(f"{what} failed ({rc}): {msg}")
+
+
+def _enqueue(logits, n: int, row_map_given: bool, bufs: _Buffers, finish, greedy: bool, sp) -> int:
+    """The stream work of one (non-debug) sampling call on stream ``sp``: the staged
+    arrays to the device, ``pbs_argmax`` (``greedy``: every row greedy with valid
+    parameters) or ``pbs_sample``, with ``finish`` (eos id, max_model_len, number of stop
+    ids) the stop check on the sampler's device tokens, and the outputs back to the pinned
+    buffer. No allocation and no memset, so the whole sequence can be captured in a graph.
+    Returns the number of output blocks copied back."""
+    lib = _lib.load()
+    cap = bufs.cap
+    words = bufs.fin if finish is None else bufs.stop_ids + finish[2]
+    bufs.d_in[:words].copy_(bufs.h_in[:words], non_blocking=True)
+    args = _args(logits, n, row_map_given, bufs)
+    out_tok = args[11]
+    if greedy:
+        _raise_for_rc(lib, lib.pbs_argmax(*args[:7], out_tok, args[12], sp), "pbs_argmax")
     else:
-        rc = lib.pbs_sample(*args, None, 0, sp)
-    if rc != _lib.OK:
-        msg = _lib.last_error(lib)
-        if rc == _lib.ERR_INVALID_ARGUMENT:
-            raise ValueError(msg)
-        if rc == _lib.ERR_UNSUPPORTED_DTYPE:
-            raise TypeError(msg)
-        what = "pbs_argmax" if greedy and not debug else "pbs_sample"
-        raise SamplerError(f"{what} failed ({rc}): {msg}")
+        _raise_for_rc(lib, lib.pbs_sample(*args, None, 0, sp), "pbs_sample")
     nout = 2
     if finish is not None:
         eos, max_model_len, nstop = finish
+        base = bufs.d_in.data_ptr()
         f = base + 4 * bufs.fin
         o = f + 4 * (cap + 1)
         rc = lib.pbs_finish_reasons(out_tok, n, -1 if eos is None else int(eos), o + 4 * 3 * cap, f,
@@ -248,13 +250,46 @@ def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, fi
             raise SamplerError(f"pbs_finish_reasons failed ({rc}): {_lib.last_error(lib)}")
         nout = 3
     bufs.h_out[: nout * cap].copy_(bufs.d_out[: nout * cap], non_blocking=True)
-    stream.synchronize()
-    if timing is not None:
-        timing["launch_sync"] = time.perf_counter()
+    return nout
+
+
+def _read_out(bufs: _Buffers, n: int, finish: bool):
+    cap = bufs.cap
     hout = bufs.h_out_np
     tokens = hout[:n].copy()
     status = hout[cap : cap + n].copy()
-    reasons = hout[2 * cap : 2 * cap + n].copy() if finish is not None else None
+    reasons = hout[2 * cap : 2 * cap + n].copy() if finish else None
+    return tokens, status, reasons
+
+
+def _launch(logits, n: int, row_map_given: bool, debug: bool, bufs: _Buffers, finish=None, timing=None,
+            greedy: bool = False):
+    """One sampling call on the current stream (``_enqueue``, or ``pbs_sample_debug`` with
+    ``debug``), then one synchronisation. Returns host tokens, statuses and reasons (None
+    without ``finish``) plus the device diagnostics of a debug call."""
+    stream = torch.cuda.current_stream(logits.device)
+    sp = stream.cuda_stream
+    probs = kept = info = None
+    if debug:
+        if finish is not None:
+            raise ValueError("the diagnostic call takes no stop check")
+        lib = _lib.load()
+        cap = bufs.cap
+        bufs.d_in[: bufs.fin].copy_(bufs.h_in[: bufs.fin], non_blocking=True)
+        args = _args(logits, n, row_map_given, bufs)
+        V = logits.shape[1]
+        probs = torch.empty((n, V), dtype=torch.float32, device=logits.device)
+        kept = torch.empty((n, V), dtype=torch.uint8, device=logits.device)
+        info = torch.empty(n * _lib.ROW_INFO_DTYPE.itemsize, dtype=torch.uint8, device=logits.device)
+        rc = lib.pbs_sample_debug(*args, probs.data_ptr(), kept.data_ptr(), info.data_ptr(), None, 0, sp)
+        _raise_for_rc(lib, rc, "pbs_sample")
+        bufs.h_out[: 2 * cap].copy_(bufs.d_out[: 2 * cap], non_blocking=True)
+    else:
+        _enqueue(logits, n, row_map_given, bufs, finish, greedy, sp)
+    stream.synchronize()
+    if timing is not None:
+        timing["launch_sync"] = time.perf_counter()
+    tokens, status, reasons = _read_out(bufs, n, finish is not None)
     return tokens, status, reasons, probs, kept, info
 
 
@@ -368,6 +403,83 @@ def sample_and_finish(logits: torch.Tensor, params: Sequence, generators: Sequen
     reasons ("stop", "length" or None) come back in the tokens' copy."""
     return _sample(logits, params, generators, rows, finish_rules=rules, eos_token_id=eos_token_id,
                    max_model_len=max_model_len)
+
+
+class SamplingGraph:
+    """One engine step's sampling call for a fixed batch, captured in a HIP graph.
+
+    The batch is fixed at construction: the logits buffer (which must keep its address,
+    e.g. a captured decode step's output, and hold the step's logits at each call), the
+    sampled rows, their parameters and, with ``finish_rules``, the stop rules' stop ids and
+    eos. The graph holds the parameters' copy to the device, ``pbs_sample`` (``pbs_argmax``
+    when every row is greedy), the stop check and the copy back; nothing in it allocates or
+    clears memory. Each call draws the rows' uniforms from their generators on the host
+    (as ``sample`` does, engine.py:138-139), writes them and the rules' per-step counts
+    into the graph's own pinned staging buffer, replays the graph and synchronises once:
+    the same tokens and reasons as ``sample_and_finish`` on the same logits and generators.
+    """
+
+    def __init__(self, logits: torch.Tensor, params: Sequence, rows: Sequence[int] | None = None,
+                 finish_rules: Sequence | None = None, eos_token_id: int | None = None, max_model_len: int = 0):
+        logits = _check_logits(logits)
+        n = len(rows) if rows is not None else logits.shape[0]
+        if n == 0:
+            raise ValueError("a sampling graph needs at least one row")
+        if len(params) != n:
+            raise ValueError(f"need {n} params, got {len(params)}")
+        if finish_rules is not None and len(finish_rules) != n:
+            raise ValueError(f"need {n} finish rules, got {len(finish_rules)}")
+        self.logits, self.n, self.rows = logits, n, rows
+        self.t, k, p = _param_arrays(params, n)
+        h = _pack(n, self.t, k, p, np.zeros(n, np.float32), rows, logits.shape[1])
+        self.greedy = _all_greedy(h)
+        self.bufs = _Buffers(logits.device)
+        nstop = sum(len(r.stop_token_ids) for r in finish_rules) if finish_rules is not None else 0
+        self.bufs.ensure(n, nstop)
+        _stage_params(self.bufs, h, n)
+        self.fin = None
+        if finish_rules is not None:
+            self.fin = (eos_token_id, max_model_len, _stage_finish(self.bufs, finish_rules, n))
+        dev = logits.device
+        # one call outside the capture (first launches), then the capture; the uniforms
+        # staged meanwhile are zeros, and no generator is touched
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            _enqueue(logits, n, rows is not None, self.bufs, self.fin, self.greedy, side.cuda_stream)
+        side.synchronize()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            _enqueue(logits, n, rows is not None, self.bufs, self.fin, self.greedy,
+                     torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize(dev)
+
+    def __call__(self, generators: Sequence[torch.Generator], finish_rules: Sequence | None = None):
+        """Tokens (and, with stop rules, reasons) of the rows for the logits the buffer holds
+        now. ``finish_rules`` (required when the graph has a stop check) may change from call
+        to call except in their total number of stop ids, which sizes the captured copy."""
+        if len(generators) != self.n:
+            raise ValueError(f"need {self.n} generators, got {len(generators)}")
+        if (finish_rules is None) != (self.fin is None):
+            raise ValueError("finish_rules must be given exactly when the graph was built with them")
+        bufs, cap, n = self.bufs, self.bufs.cap, self.n
+        u = _uniforms(self.t, generators)
+        bufs.h_in_np[_IN_U * cap : _IN_U * cap + n] = u.view(np.int32)
+        if finish_rules is not None:
+            if len(finish_rules) != n:
+                raise ValueError(f"need {n} finish rules, got {len(finish_rules)}")
+            if _stage_finish(bufs, finish_rules, n) != self.fin[2]:
+                raise ValueError("the number of stop ids changed since the graph was captured")
+        self.graph.replay()
+        torch.cuda.current_stream(self.logits.device).synchronize()
+        tokens, status, reasons = _read_out(bufs, n, self.fin is not None)
+        _raise_for_status(status, self.t)
+        if self.fin is None:
+            return tokens.tolist(), None
+        from .finish import REASONS
+
+        return tokens.tolist(), [REASONS[c] for c in reasons.tolist()]
 
 
 def sample_token(logits: torch.Tensor, params, generator: torch.Generator) -> int:

@@ -100,3 +100,44 @@ def test_graph_replay_equals_eager_decode(dev, fused_head):
     for ce, cg in zip(te.captures, tg.captures):
         assert ce.step == cg.step
         assert torch.equal(ce.logits.view(torch.int16), cg.logits.view(torch.int16)), f"step {ce.step}"
+
+
+def test_sampling_graph_matches_the_eager_call(dev):
+    """sampling.SamplingGraph against sample_and_finish on the same logits buffer and the
+    same generator states, over several replays with new logits, eager sampler calls and
+    synchronisations between them; bf16 and fp32 logits, mixed rows, a row map, stop ids."""
+    from pagedbatch_amd import SamplingGraph, SamplingParams, sample_and_finish
+    from pagedbatch_amd.finish import FinishRule
+
+    g = torch.Generator().manual_seed(5)
+    for dtype in (torch.bfloat16, torch.float32):
+        print(f"[case] sampling graph {dtype}", flush=True)
+        B, V = 12, 3000
+        buf = torch.empty(B, V, dtype=dtype, device=dev)
+        rows = [0, 2, 3, 5, 7, 8, 9, 11]
+        params = [SamplingParams(temperature=0.0), SamplingParams(temperature=0.7, top_k=20),
+                  SamplingParams(temperature=1.0, top_p=0.9), SamplingParams(temperature=1.3),
+                  SamplingParams(temperature=0.0), SamplingParams(temperature=1.0, top_k=5, top_p=0.8),
+                  SamplingParams(temperature=0.9, top_p=0.95), SamplingParams(temperature=1.1, top_k=100)]
+        shared = torch.Generator().manual_seed(11)
+        seeded = torch.Generator().manual_seed(12)
+        gens = [shared, shared, seeded, shared, shared, shared, seeded, shared]
+
+        def rules(step):
+            return [FinishRule(ignore_eos=(i % 3 == 0), stop_token_ids=(7, 11 + i), num_output=step + 1,
+                               max_tokens=4, num_tokens=20 + step) for i in range(len(rows))]
+
+        sg = SamplingGraph(buf, params, rows=rows, finish_rules=rules(0), eos_token_id=2, max_model_len=64)
+        for step in range(4):
+            x = torch.randn(B, V, generator=g) * 3.0
+            x[:, 7] = 30.0 if step == 2 else x[:, 7]   # a step whose greedy rows hit a stop id
+            buf.copy_(x.to(dtype))
+            ref_state = [shared.get_state(), seeded.get_state()]
+            want = sample_and_finish(buf, params, gens, rules(step), 2, 64, rows=rows)
+            shared.set_state(ref_state[0])
+            seeded.set_state(ref_state[1])
+            got = sg(gens, rules(step))
+            assert got == want, f"step {step}: {got} != {want}"
+            torch.cuda.synchronize()
+            sample_and_finish(buf, params, [torch.Generator().manual_seed(99)] * len(rows), rules(step), 2, 64,
+                              rows=rows)  # eager work between replays
