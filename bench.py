@@ -13,7 +13,8 @@ rocprofv3 kernel trace reports). Each launch is also timed on its own with an ev
 (``us_per_launch_events``, which also spans the launch's dispatch), and the Python
 ``sample()`` surface per step is reported as ``us_per_step_python`` (256 seeded
 generators) with its split into uniforms, packing and launch + copy back + sync for one
-shared generator and for 256 seeded ones (``python_surface``).
+shared generator and for 256 seeded ones, and for the same call replayed from a HIP graph
+(``python_surface``).
 
 ``--workload engine_step_smollm2`` instead runs the end-to-end engine step
 (pagedbatch_amd/engine_step.py) and reports decode tokens/s and the sampler's share.
@@ -174,6 +175,23 @@ def python_surface(w, bufs, copies, rows):
             parts["launch_sync_us"].append(tm["launch_sync"] - tm["pack"])
             parts["total_us"].append(t1 - t0)
         out[name] = {k: round(statistics.median(v) * 1e6, 1) for k, v in parts.items()}
+    # the same call captured in a HIP graph (sampling.SamplingGraph on one fixed logits
+    # buffer): per step only the uniforms, the replay and one synchronisation
+    from pagedbatch_amd import SamplingGraph
+
+    for name in ("shared_generator_graph", "seeded_generators_graph"):
+        shared = torch.Generator().manual_seed(0)
+        gens = [shared] * rows if name.startswith("shared") else [torch.Generator().manual_seed(i)
+                                                                  for i in range(rows)]
+        sg = SamplingGraph(bufs[0], sp)
+        for i in range(3):
+            sg(gens)
+        ts = []
+        for i in range(20):
+            t0 = time.perf_counter()
+            sg(gens)
+            ts.append(time.perf_counter() - t0)
+        out[name] = {"total_us": round(statistics.median(ts) * 1e6, 1)}
     return out
 
 
