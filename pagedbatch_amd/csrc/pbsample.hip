@@ -2263,16 +2263,25 @@ __device__ __forceinline__ uint32_t find_bin_bound(const Smem& s, uint32_t lo, d
 
 // One pass over the row: every element whose bin lies in one of the NW windows [lo_i,
 // hi_i] (they may overlap) goes into L, unsorted; above_i gets the exact mass of the
-// elements in bins above window i. Each wave appends to its own segment of SEG entries
-// (ballot and lane rank: no atomics). Returns false if a segment overflowed.
+// elements in bins above window i. Each wave fills its own segment of SEG entries, no
+// atomics, in one of two ways:
+//   cols: every lane appends to its own column of the segment (entry slot * 64 + lane,
+//     COL_CAP slots, a full lane writing on into a spare last slot), with no cross-lane
+//     work per element; one pass at the end compacts the columns into the segment's
+//     first entries, slot by slot. Returns false if a column overflowed.
+//   otherwise: a ballot and lane ranks per element whose vector holds an entry.
+// Returns false if a segment overflowed. The list's order is irrelevant to its readers.
+constexpr uint32_t COL_CAP = SEG / 64 - 1;  // entries per lane column (the last slot is spare)
 template <int DT, int NW, class Src, class Div>
 __device__ __forceinline__ bool gather_bins(const Src& src, Smem& s, uint64_t* L, const Div& dv, float m,
                                                 uint32_t lo0, uint32_t hi0, uint32_t lo1, uint32_t hi1,
                                                 uint32_t lo2, uint32_t hi2, double& above0, double& above1,
-                                                double& above2) {
+                                                double& above2, bool cols) {
   const uint32_t lo[3] = {lo0, lo1, lo2}, hi[3] = {hi0, hi1, hi2};
   uint64_t* const seg = L + wave_id() * SEG;
+  const uint32_t ln = (uint32_t)lane_id();
   uint32_t wn = 0u;  // entries the wave appended (uniform)
+  uint32_t lc = 0u;  // cols: entries this lane appended (may pass COL_CAP: overflow)
   __syncthreads();   // the histogram the list overwrites is no longer read
   double acc[NW];
 #pragma unroll
@@ -2303,7 +2312,15 @@ __device__ __forceinline__ bool gather_bins(const Src& src, Smem& s, uint64_t* L
         in[e] = vvalid && hit;
         any = any || in[e];
       }
-      if (ballot(any)) {
+      if (cols) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (in[e]) {
+            seg[min(lc, COL_CAP) * 64u + ln] = ((uint64_t)(~key[e]) << 32) | (uint32_t)(base + e);
+            ++lc;
+          }
+        }
+      } else if (ballot(any)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint64_t bal = ballot(in[e]);
@@ -2352,12 +2369,53 @@ __device__ __forceinline__ bool gather_bins(const Src& src, Smem& s, uint64_t* L
   above0 = tot[0];
   above1 = tot[1];
   above2 = tot[2];
+  if (cols) {
+    if (ballot(lc > COL_CAP)) {
+      wn = SEG + 1u;  // a column overflowed: the caller gathers again with ballots
+    } else {
+      // slot by slot, the entries of the lanes that have one move to the next free entries
+      // of the segment: every destination lies at or before its source (at most 64 entries
+      // per earlier slot went before it), in a slot already read
+      const uint32_t nslot = wmax_u32(lc);
+      for (uint32_t k = 0u; k < nslot; ++k) {
+        const bool has = k < lc;
+        const uint64_t bal = ballot(has);
+        if (has) {
+          const uint64_t e = seg[k * 64u + ln];
+          seg[wn + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] = e;
+        }
+        wn += (uint32_t)__popcll(bal);
+      }
+    }
+  }
   if (lane_id() == 0) s.seg_n[wave_id()] = wn;
   __syncthreads();
   bool ok = true;
 #pragma unroll
   for (int w = 0; w < NWAVE; ++w) ok = ok && s.seg_n[w] <= SEG;
   return ok;
+}
+
+// gather_bins with lane columns when the windows are dense (one element in 256 or more, so
+// that most of the wave's 256-element vectors hold an entry and the ballot path's skip of
+// empty vectors saves little) and hold few enough elements that no column should fill (at
+// most 12 per lane on average, against COL_CAP); else with ballots. A column that overflows anyway
+// (entries crowded into few lanes) costs one more pass with ballots. The histogram must
+// still be intact (the counts decide).
+constexpr uint32_t COLS_MAX = 12u * NT;
+template <int DT, int NW, class Src, class Div>
+__device__ __forceinline__ bool gather_windows(const Src& src, Smem& s, uint64_t* L, const Div& dv, float m,
+                                               uint32_t lo0, uint32_t hi0, uint32_t lo1, uint32_t hi1,
+                                               uint32_t lo2, uint32_t hi2, double& above0, double& above1,
+                                               double& above2) {
+  const uint32_t lo[3] = {lo0, lo1, lo2}, hi[3] = {hi0, hi1, hi2};
+  uint32_t n_in = 0u;  // elements in the windows, counted once per window they lie in
+#pragma unroll
+  for (int r = 0; r < NW; ++r) n_in += count_bins_ge(s, lo[r]) - count_bins_ge(s, hi[r] + 1u);
+  const bool cols = Src::kVector && n_in <= COLS_MAX && (uint64_t)n_in * 256u >= (uint64_t)src.vocab;
+  if (gather_bins<DT, NW>(src, s, L, dv, m, lo0, hi0, lo1, hi1, lo2, hi2, above0, above1, above2, cols))
+    return true;
+  return cols && gather_bins<DT, NW>(src, s, L, dv, m, lo0, hi0, lo1, hi1, lo2, hi2, above0, above1, above2, false);
 }
 
 // count and fixed-point mass (FIXQ units, exact) of the list's entries in [ea, eb]; each
@@ -2681,7 +2739,7 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     // Everything from the k-th element's bin up fits in one list: the whole row resolves
     // from it (two passes over the row in all).
     double a0, a1, a2;
-    if (!gather_bins<DT, 1>(src, s, big, dv, m, klo, 0xffffu, 0u, 0u, 0u, 0u, a0, a1, a2)) return false;
+    if (!gather_windows<DT, 1>(src, s, big, dv, m, klo, 0xffffu, 0u, 0u, 0u, 0u, a0, a1, a2)) return false;
     const Pick pk = list_pick<false>(s, big, 0ull, ~0ull, m, 0.0, (double)(kk - 1));
     if (pk.e == ~0ull) return false;
     const uint32_t kmin = key_of(pk.e);
@@ -2760,10 +2818,10 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   // windows: the draw's, then the cutoff's and the k-th element's bin when they apply
   double above_d, above_c = 0.0, above_k = 0.0, a2;
   bool fits;
-  if (cut && topk) fits = gather_bins<DT, 3>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, klo, klo, above_d, above_c, above_k);
-  else if (cut) fits = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, 0u, 0u, above_d, above_c, a2);
-  else if (topk) fits = gather_bins<DT, 2>(src, s, big, dv, m, dlo, dhi, klo, klo, 0u, 0u, above_d, above_k, a2);
-  else fits = gather_bins<DT, 1>(src, s, big, dv, m, dlo, dhi, 0u, 0u, 0u, 0u, above_d, a2, a2);
+  if (cut && topk) fits = gather_windows<DT, 3>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, klo, klo, above_d, above_c, above_k);
+  else if (cut) fits = gather_windows<DT, 2>(src, s, big, dv, m, dlo, dhi, c_lo, c_hi, 0u, 0u, above_d, above_c, a2);
+  else if (topk) fits = gather_windows<DT, 2>(src, s, big, dv, m, dlo, dhi, klo, klo, 0u, 0u, above_d, above_k, a2);
+  else fits = gather_windows<DT, 1>(src, s, big, dv, m, dlo, dhi, 0u, 0u, 0u, 0u, above_d, a2, a2);
   if (!fits) return false;
   double dummy;
 

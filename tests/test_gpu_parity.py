@@ -288,6 +288,28 @@ def test_fp32_window_paths(dev):
     run_case(dev, "fp32_window_paths", x, T, K, P, U, want_probs=False, info_only=True)
 
 
+@pytest.mark.parametrize("V", [49152, 151936])
+def test_fp32_windows_crowded_into_one_lane(dev, V):
+    """fp32 rows whose windows are dense (the largest values, which hold the top-k, the
+    top-p cutoff and the draw, are one element in 40) with every element of one thread
+    among them (element i belongs to thread (i // 4) % 512): that lane's list column
+    overflows, so the gather runs again with ballots. Registers (V = 49152) and the
+    re-read row (V = 151936)."""
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(4, V, generator=g) * 0.5
+    t0 = 5
+    idx = torch.tensor([4 * (t0 + 512 * k) + e for k in range((V // 4 + 511) // 512) for e in range(4)
+                        if 4 * (t0 + 512 * k) + e < V])
+    others = torch.tensor(sorted(set(torch.randperm(V, generator=g)[: V // 40].tolist()) - set(idx.tolist())))
+    top = torch.cat([idx, others])
+    x[:, top] = 8.0 + torch.randn(4, len(top), generator=g) * 0.01
+    T = [1.0, 1.0, 0.7, 1.0]
+    K = [64, 0, 0, 30]
+    P = [1.0, 0.5, 0.9, 0.8]
+    U = [float(v) for v in torch.rand(4, generator=g)]
+    run_case(dev, f"fp32_crowded_lane_{V}", x, T, K, P, U, want_probs=V <= 49152, info_only=V > 49152)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_register_row_sizes(dev, dtype):
     """Vocab sizes that land on each register-row width (and just past the largest)."""
