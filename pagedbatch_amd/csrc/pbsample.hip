@@ -2786,19 +2786,37 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   // in bins [c_lo, c_hi]. Z_P, its inclusive mass, lies in (tau, tau + its weight], which
   // bounds the draw's target u Z_P (u Z_K without a cutoff): the draw lies in bins
   // [d_lo, d_hi]. Every window lies at or above klo.
+  // Each pair of searches (the bounds on Z_K, the cutoff's window, the draw's window) runs
+  // in waves 0 and 1 side by side, the two results handed over in LDS (s.red_d, s.red_i):
+  // the same calls on the same state as in one wave, so the same results.
   double zlo = z_all, zhi = z_all;
   if (topk) {
     float wl, wh;
     bin_bounds(klo, m, wl, wh);
-    zlo = bound_above<false>(s, klo, m) + (double)(kk - (int)kabove) * (double)wl;
-    zhi = bound_above<true>(s, klo, m) + (double)kc * (double)wh;
+    if (wv == 0) {
+      const double b0 = bound_above<false>(s, klo, m);
+      if (l == 0) s.red_d[0] = b0;
+    } else if (wv == 1) {
+      const double b1 = bound_above<true>(s, klo, m);
+      if (l == 0) s.red_d[1] = b1;
+    }
+    __syncthreads();
+    zlo = s.red_d[0] + (double)(kk - (int)kabove) * (double)wl;
+    zhi = s.red_d[1] + (double)kc * (double)wh;
   }
   uint32_t c_lo = 0u, c_hi = 0u;
   double t_lo, t_hi;
   if (cut) {
     const double tau_lo = (double)p * zlo * (1.0 - 1e-6), tau_hi = (double)p * zhi * (1.0 + 1e-6);
-    const uint32_t ob = find_bin_bound<true>(s, klo, tau_lo, m);
-    const uint32_t oa = find_bin_bound<false>(s, klo, tau_hi, m);
+    if (wv == 0) {
+      const uint32_t ob = find_bin_bound<true>(s, klo, tau_lo, m);
+      if (l == 0) s.red_i[0] = (int)ob;
+    } else if (wv == 1) {
+      const uint32_t oa = find_bin_bound<false>(s, klo, tau_hi, m);
+      if (l == 0) s.red_i[1] = (int)oa;
+    }
+    __syncthreads();
+    const uint32_t ob = (uint32_t)s.red_i[0], oa = (uint32_t)s.red_i[1];
     c_lo = min(oa, ob);
     c_hi = max(oa, ob);
     float wl, wh;
@@ -2809,8 +2827,15 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     t_lo = (double)u * zlo * (1.0 - 1e-6);
     t_hi = (double)u * zhi * (1.0 + 1e-6);
   }
-  const uint32_t d_hi = find_bin_bound<true>(s, klo, t_lo, m);
-  const uint32_t d_lo = find_bin_bound<false>(s, klo, t_hi, m);
+  if (wv == 0) {
+    const uint32_t r = find_bin_bound<true>(s, klo, t_lo, m);
+    if (l == 0) s.red_i[2] = (int)r;
+  } else if (wv == 1) {
+    const uint32_t r = find_bin_bound<false>(s, klo, t_hi, m);
+    if (l == 0) s.red_i[3] = (int)r;
+  }
+  __syncthreads();
+  const uint32_t d_hi = (uint32_t)s.red_i[2], d_lo = (uint32_t)s.red_i[3];
   const uint32_t dlo = min(d_lo, d_hi), dhi = max(d_lo, d_hi);
   // every element above the cutoff window is in K (the window lies at or above klo)
   const uint32_t n_above_c = cut ? count_bins_ge(s, c_hi + 1u) : 0u;
