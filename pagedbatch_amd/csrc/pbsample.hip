@@ -2582,6 +2582,9 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
   const int V = a.vocab;
   const int l = lane_id(), wv = wave_id();
   uint64_t* const big = (uint64_t*)s.hist;  // the list, once the histogram is no longer read
+  // the kept-set counts (ties kept at the cutoff, kept elements) only feed the row
+  // diagnostics: without them the list passes that count them are skipped
+  const bool diag = a.out_info != nullptr;
 
   // stream: histogram, row maximum, NaN, and sum_i exp(x_i - xmax) with the thread's
   // running maximum xmax (rescaled once per 16-byte vector)
@@ -2746,24 +2749,26 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     const uint64_t eK = e_last(kmin);
     st.x_kth = float_of_ord32(kmin);
     st.kord_lo = kmin;
-    uint32_t nK, kties;
+    uint32_t nK, kties = 0u;
     double zq, dummy;
     list_sum<true>(s, big, 0ull, eK, m, nK, zq);
-    list_sum<false>(s, big, e_first(kmin), eK, m, kties, dummy);
+    if (diag) list_sum<false>(s, big, e_first(kmin), eK, m, kties, dummy);
     st.zk = zq * FIXQ;
     uint64_t eD = eK;  // the draw's last candidate
     if (cut) {
       const Pick pc = list_pick<true>(s, big, 0ull, eK, m, 0.0, (double)p * st.zk);
       if (pc.e == ~0ull) return false;
       const uint32_t ckey = key_of(pc.e);
-      uint32_t nkept, ntie, nkeep;
-      list_sum<false>(s, big, 0ull, pc.e, m, nkept, dummy);
-      list_sum<false>(s, big, e_first(ckey), e_last(ckey), m, ntie, dummy);
-      list_sum<false>(s, big, e_first(ckey), pc.e, m, nkeep, dummy);
+      if (diag) {
+        uint32_t nkept, ntie, nkeep;
+        list_sum<false>(s, big, 0ull, pc.e, m, nkept, dummy);
+        list_sum<false>(s, big, e_first(ckey), e_last(ckey), m, ntie, dummy);
+        list_sum<false>(s, big, e_first(ckey), pc.e, m, nkeep, dummy);
+        st.n_cut_tie = (int)ntie;
+        st.n_cut_keep = (int)nkeep;
+        st.n_kept = (int)nkept;
+      }
       st.x_cut = float_of_ord32(ckey);
-      st.n_cut_tie = (int)ntie;
-      st.n_cut_keep = (int)nkeep;
-      st.n_kept = (int)nkept;
       st.zp = pc.excl + pc.w;
       eD = pc.e;
     } else {
@@ -2861,13 +2866,13 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     eK = e_last(kmin);
     st.x_kth = float_of_ord32(kmin);
     st.kord_lo = kmin;
-    uint32_t cnt, kties;
+    uint32_t cnt, kties = 0u;
     double zq;
     // Z_K: the mass above bin klo, plus its entries down to the last of K
     list_sum<true>(s, big, e_bins_first(klo), eK, m, cnt, zq);
     zk = above_k + zq * FIXQ;
     nk = kabove + cnt;
-    list_sum<false>(s, big, e_first(kmin), eK, m, kties, dummy);
+    if (diag) list_sum<false>(s, big, e_first(kmin), eK, m, kties, dummy);
     st.x_cut = st.x_kth;
     st.n_cut_tie = st.n_cut_keep = (int)kties;
   } else {
@@ -2886,14 +2891,16 @@ __device__ __forceinline__ bool sample_row32(const KArgs& a, Smem& s, Src0& src0
     if (pc.e == ~0ull) return false;
     ec = pc.e;
     const uint32_t ckey = key_of(ec);
-    uint32_t cnt, ntie, nkeep;
-    list_sum<false>(s, big, ea, ec, m, cnt, dummy);
-    list_sum<false>(s, big, e_first(ckey), e_last(ckey), m, ntie, dummy);
-    list_sum<false>(s, big, e_first(ckey), ec, m, nkeep, dummy);
+    if (diag) {
+      uint32_t cnt, ntie, nkeep;
+      list_sum<false>(s, big, ea, ec, m, cnt, dummy);
+      list_sum<false>(s, big, e_first(ckey), e_last(ckey), m, ntie, dummy);
+      list_sum<false>(s, big, e_first(ckey), ec, m, nkeep, dummy);
+      st.n_cut_tie = (int)ntie;
+      st.n_cut_keep = (int)nkeep;
+      st.n_kept = (int)(n_above_c + cnt);
+    }
     st.x_cut = float_of_ord32(ckey);
-    st.n_cut_tie = (int)ntie;
-    st.n_cut_keep = (int)nkeep;
-    st.n_kept = (int)(n_above_c + cnt);
     st.zp = pc.excl + pc.w;
   }
   // the draw (sampling.py:26-27, inverse-CDF form): in the cutoff window, up to the
