@@ -631,14 +631,15 @@ struct RegRow {
     nvec = nvec_;
     vocab = vocab_;
   }
-  // Raw buffer loads: one VGPR offset (the thread's) for every chunk, the chunk offset in
-  // an SGPR, and the buffer's range check returning zeros past the row end, so the code
-  // stays straight-line and the compiler waits for each chunk only when it is first used.
-  // Non-temporal: the row is read from memory exactly once.
+  // Raw buffer loads whose whole offset is in the VGPR operand, so the buffer's range check
+  // returns zeros past the row end (the check covers that operand; nothing is read past the
+  // row), the code stays straight-line and the compiler waits for each chunk only when it
+  // is first used. Non-temporal: the row is read from memory exactly once.
   __device__ __forceinline__ void load_chunk(int j) {
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, nvec * 16, 0x00020000);
-    r[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, j * NT * 16, 2));
+    r[j] = __builtin_bit_cast(
+        u4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(j * NT + (int)threadIdx.x) * 16u, 0, 2));
   }
   // issues the first D chunks; stream() issues the rest as it consumes the row
   __device__ __forceinline__ void load() {
@@ -683,16 +684,19 @@ struct MemRow {
     vocab = vocab_;
   }
   __device__ __forceinline__ void load() {}
-  // Every pass streams the row again: raw buffer loads (range-checked, zeros past the end)
-  // four chunks per step, the next four issued before the current four are used, so eight
-  // loads per thread are in flight instead of one.
+  // Every pass streams the row again: raw buffer loads four chunks per step, the next four
+  // issued before the current four are used, so eight loads per thread are in flight
+  // instead of one. The whole offset is in the VGPR operand, so the buffer's range check
+  // returns zeros for the chunks past the row end that the last step reads ahead, and
+  // nothing past the row is read.
   template <class F>
   __device__ __forceinline__ void for_each(F&& f) const {
     const int nch = (nvec + NT - 1) / NT;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, nvec * 16, 0x00020000);
     auto ld = [&](int j) {
-      return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16u, j * NT * 16, 0));
+      return __builtin_bit_cast(
+          u4, __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(j * NT + (int)threadIdx.x) * 16u, 0, 0));
     };
     u4 a0 = ld(0), a1 = ld(1), a2 = ld(2), a3 = ld(3);
     for (int j = 0; j < nch; j += 4) {
