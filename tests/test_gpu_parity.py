@@ -288,6 +288,29 @@ def test_fp32_window_paths(dev):
     run_case(dev, "fp32_window_paths", x, T, K, P, U, want_probs=False, info_only=True)
 
 
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 128256), (torch.float16, 128256), (torch.bfloat16, 200000)])
+def test_rows_masked_with_neg_inf(dev, dtype, V):
+    """Rows whose vocabulary is masked with -inf (more than 65535 entries, so -inf's u16
+    counter wraps): they resolve from the histogram with -inf's exact count. Greedy rows,
+    top-k inside and past the finite entries (the k-th is then -inf and everything is
+    kept), top-p, temperatures, and a row where 70000 zeros wrap a finite counter too,
+    which takes the general path. Registers (V = 128256) and the re-read row (200000)."""
+    g = torch.Generator().manual_seed(41)
+    rows = 8
+    nfin = [1000, 500, 3000, 800, 20, 2000, 1500, 600]
+    x = torch.full((rows, V), float("-inf"))
+    for r in range(rows):
+        keep = torch.randperm(V, generator=g)[: nfin[r]]
+        x[r, keep] = torch.randn(nfin[r], generator=g) * 2.0
+    zeros = torch.randperm(V, generator=g)[:70000]
+    x[7, zeros] = 0.0
+    T = [0.0, 1.0, 0.8, 1.0, 1.0, 0.6, 1.2, 1.0]
+    K = [0, 0, 20, 5000, 50, 0, 100, 0]
+    P = [1.0, 1.0, 0.9, 1.0, 0.95, 0.8, 1.0, 0.9]
+    U = [float(v) for v in torch.rand(rows, generator=g)]
+    run_case(dev, f"masked_{DT_NAME[dtype]}_{V}", x.to(dtype), T, K, P, U, want_probs=False)
+
+
 @pytest.mark.parametrize("V", [49152, 151936])
 def test_fp32_windows_crowded_into_one_lane(dev, V):
     """fp32 rows whose windows are dense (the largest values, which hold the top-k, the
