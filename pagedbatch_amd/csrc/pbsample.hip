@@ -1496,43 +1496,6 @@ __device__ __forceinline__ TieGroup tie_group(const Smem& s, const BinHit& h, ui
   return t;
 }
 
-// the raw pattern of -inf
-template <int DT>
-__device__ __forceinline__ uint32_t neg_inf_raw16() {
-  return DT == PBS_DTYPE_BF16 ? 0xff80u : 0xfc00u;
-}
-// elements of the row whose raw pattern is raw (the whole workgroup, one pass; barriers)
-template <int DT, class Src>
-__device__ __forceinline__ uint32_t count_raw16(const Src& src, Smem& s, uint32_t raw) {
-  constexpr int EPV = DTraits<DT>::EPV;
-  uint32_t c = 0u;
-  if constexpr (Src::kVector) {
-    // per 16-byte vector: eight elements less its misses (packed, as the selection counts)
-    const uint32_t raw2 = raw | (raw << 16);
-    uint32_t one2 = 0x00010001u;
-    asm("" : "+v"(one2));
-    src.for_each([&](int, const u4& q, int, bool vvalid) {
-      const uint32_t miss = lane_misses16<false, true>(q, raw2, 0u, one2);
-      c += vvalid ? 8u - miss : 0u;
-    });
-  } else {
-    src.for_each([&](int, const u4& q, int base, bool vvalid) {
-#pragma unroll
-      for (int e = 0; e < EPV; ++e)
-        c += (elem_valid(src, vvalid, base + e) && elem_raw<DT>(q, e) == raw) ? 1u : 0u;
-    });
-  }
-  c = wsum_u32(c);
-  __syncthreads();  // every wave is past its last read of the reduction slots
-  if (lane_id() == 0) s.red_i[wave_id()] = (int)c;
-  __syncthreads();
-  uint32_t t = 0u;
-#pragma unroll
-  for (int w = 0; w < NWAVE; ++w) t += (uint32_t)s.red_i[w];
-  __syncthreads();
-  return t;
-}
-
 // The k-th largest element by counts alone (before any mass is known): its ord, the ord
 // range of its tie group, the group's count and the count above it. Wave-local: the
 // counts above each group come from a wave scan of the group counts.
@@ -1599,9 +1562,8 @@ __device__ __forceinline__ KthCount kth_by_count(const Smem& s, uint32_t need, c
 // s.res_ok = 0 if a u16 counter wrapped (one value more than 65535 times) or a search
 // found nothing: the caller then takes the general path.
 template <int DT>
-__device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int kk, const KthCount& kc,
-                                          const KthCount& ninf, float p, float u, float m, bool want_info,
-                                          RowState& st) {
+__device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int kk, const KthCount& kc, float p,
+                                          float u, float m, bool want_info, RowState& st) {
   // Wave 0 searches (and wave 1 beside it, for the guessed draw): the other waves wait at
   // the barriers instead of competing for their SIMDs' issue slots with copies of the same
   // work (waves w and w + 4 share a SIMD). Wave 0 leaves the selection in s.res_*, which
@@ -1671,19 +1633,10 @@ __device__ __forceinline__ void resolve16(Smem& s, int V, const Divider& dv, int
     // all of K is kept; the cutoff group is K's lowest value (for the diagnostics only: the
     // draw below searches all of K)
     if (!topk && want_info) {
-      if (ninf.ok) {
-        // the lowest tie group is -inf's, whose bin count wrapped: its exact size
-        ct.lo = ninf.lo;
-        ct.hi = ninf.hi;
-        ct.n = ninf.n;
-        ct.n_above = ninf.n_above;
-        ct.above = zk;
-        ct.w = 0.0;
-      } else if (find_by_count<DT>(s, nk, dv, m, h)) {
+      if (find_by_count<DT>(s, nk, dv, m, h))
         ct = tie_group<DT>(s, h, 0u, dv, m);
-      } else {
+      else
         ok = false;
-      }
     }
     n_keep = (int)ct.n;
     zp = zk;
@@ -1788,45 +1741,12 @@ __device__ __forceinline__ void hist_group_counts(Smem& s) {
 // Returns false when the general path must take the row (a u16 counter wrapped).
 template <int DT, class Src>
 __device__ __forceinline__ bool tail16(const KArgs& a, Smem& s, Src& src, int b, const Divider& dv, float m, int kk,
-                                       float p, float u, bool has_ninf) {
+                                       float p, float u) {
   const int V = a.vocab;
   const int l = lane_id(), wv = wave_id();
 
   hist_group_counts<DT>(s);
   __syncthreads();
-
-  // A row masked with -inf (more than 65535 of them) wraps -inf's u16 counter. -inf has
-  // no mass, so the row resolves from the histogram all the same once -inf's group count
-  // holds the exact number (counted again from the row) and the two count searches that
-  // can land on -inf's tie group (a top-k past the elements above it, the diagnostics'
-  // lowest tie group) take that group directly. Any other wrapped counter still sends the
-  // row to the general path.
-  KthCount ninf = {};  // -inf's tie group when its counter was corrected (ok set)
-  if (has_ninf) {
-    uint32_t c = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c += s.gcount[4 * l + i];
-    const uint32_t tot = uni_u32(wsum_u32(c));
-    if (tot != (uint32_t)V) {
-      // -inf's counter is the low half of its word (the raw is even): it kept n mod 2^16
-      // and carried n >> 16 into the high half, the counter of raw + 1, a NaN pattern that
-      // no accepted row holds (and whose count would give its group a NaN mass)
-      const uint32_t raw = neg_inf_raw16<DT>();
-      const uint32_t n_ni = count_raw16<DT>(src, s, raw);
-      const uint32_t kept = n_ni & 0xffffu, carried = n_ni >> 16;
-      if (tot - kept - carried + n_ni != (uint32_t)V) return false;  // another counter wrapped
-      if (threadIdx.x == 0) {
-        s.hist[raw >> 1] &= 0xffffu;
-        s.gcount[ord16u(raw) >> 8] += n_ni - kept - carried;
-      }
-      __syncthreads();
-      ninf.o = ord16u(raw);
-      tie_range16<DT>(ninf.o, dv, ninf.lo, ninf.hi);
-      ninf.n_above = count_ge_local(s, ninf.hi + 1u);
-      ninf.n = (uint32_t)V - ninf.n_above;
-      ninf.ok = true;
-    }
-  }
 
   // top-k (sampling.py:15-17): the k-th element by counts; only its tie group and the
   // groups above it (K) need masses
@@ -1834,7 +1754,7 @@ __device__ __forceinline__ bool tail16(const KArgs& a, Smem& s, Src& src, int b,
   KthCount kc = {};
   uint32_t glo = 0u;
   if (topk) {
-    kc = (ninf.ok && (uint32_t)kk > ninf.n_above) ? ninf : kth_by_count<DT>(s, (uint32_t)kk, dv);
+    kc = kth_by_count<DT>(s, (uint32_t)kk, dv);
     if (!kc.ok) return false;
     glo = kc.lo >> 8;
   }
@@ -1901,7 +1821,7 @@ __device__ __forceinline__ bool tail16(const KArgs& a, Smem& s, Src& src, int b,
   }
   __syncthreads();
   RowState st;
-  resolve16<DT>(s, V, dv, kk, kc, ninf, p, u, m, a.out_info != nullptr, st);
+  resolve16<DT>(s, V, dv, kk, kc, p, u, m, a.out_info != nullptr, st);
   __syncthreads();
   if (!s.res_ok) return false;  // a counter wrapped
 
@@ -1986,7 +1906,7 @@ __device__ __forceinline__ bool sample_row16(const KArgs& a, Smem& s, Src& src, 
     return true;
   }
 
-  return tail16<DT>(a, s, src, b, dv, m, kk, p, u, omin == ord16u(neg_inf_raw16<DT>()));
+  return tail16<DT>(a, s, src, b, dv, m, kk, p, u);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -291,10 +291,10 @@ def test_fp32_window_paths(dev):
 @pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 128256), (torch.float16, 128256), (torch.bfloat16, 200000)])
 def test_rows_masked_with_neg_inf(dev, dtype, V):
     """Rows whose vocabulary is masked with -inf (more than 65535 entries, so -inf's u16
-    counter wraps): they resolve from the histogram with -inf's exact count. Greedy rows,
-    top-k inside and past the finite entries (the k-th is then -inf and everything is
-    kept), top-p, temperatures, and a row where 70000 zeros wrap a finite counter too,
-    which takes the general path. Registers (V = 128256) and the re-read row (200000)."""
+    counter wraps and the rows take the general path): greedy rows, top-k inside and past
+    the finite entries (the k-th is then -inf and everything is kept), top-p,
+    temperatures, and a row where 70000 zeros wrap a finite counter too. Registers
+    (V = 128256) and the re-read row (200000)."""
     g = torch.Generator().manual_seed(41)
     rows = 8
     nfin = [1000, 500, 3000, 800, 20, 2000, 1500, 600]
